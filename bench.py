@@ -1,0 +1,157 @@
+"""Benchmark: batch-1 greedy decode of a Qwen3-8B-shape Q4_K_M model on one MI355X.
+
+Workload: hidden 4096, 36 layers, 32 q / 8 KV heads x 128,
+q/k RMSNorm, SwiGLU FFN 12288, vocab 151936, rope theta 1e6; Q4_K matrices with
+Q6_K for attn_v, ffn_down and output, Q4_K token_embd; seeded N(0, 0.02) weights
+quantized by the library's GGML block quantizer (synthetic data: no network).
+A 512-token random prompt, then greedy decode. One "step" = one decoded token
+(one HIP-graph replay of the whole per-token chain); K steps are timed with HIP
+events on the decode stream after W warmup steps.
+
+Prints one JSON line: decode tok/s (value), prefill tok/s, the roofline of the
+dominant kernel (fused gate/up Q4_K dequant-matvec, HIP-event timed live), and the
+CPU baseline (the oracle's host dequant+matvec restatement over one layer + head).
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+CFG = dict(qwen3=True, hidden=4096, layers=36, q_heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=151936,
+           rope_base=1e6, rms_eps=1e-6, weight_std=0.02, seed=0)
+
+
+def algorithmic_bytes_per_token(info, ctx_mean):
+    """Encoded weight bytes streamed per token + one embedding row + norms + BF16 KV read/write."""
+    H, L, hkv, hd, V = info.hidden, info.layers, info.kv_heads, info.head_dim, info.vocab
+    embd_row = H // 256 * 144
+    norms = (2 * L + 1) * H * 4 + 2 * L * hd * 4
+    weights = info.weight_bytes - V * (H // 256) * 144 + embd_row   # token_embd is gathered, not streamed
+    kv = ctx_mean * 2 * L * hkv * hd * 2 + 2 * L * hkv * hd * 2
+    return weights + norms + kv, weights
+
+
+def cpu_baseline(path, info):
+    """Oracle host dequant+matvec (restating dequantize_block + gguf_gemv) over layer 0 and the head."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle_ffi as orc
+    g = orc.Gguf(path)
+    names = ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.attn_v.weight", "blk.0.attn_output.weight",
+             "blk.0.ffn_gate.weight", "blk.0.ffn_up.weight", "blk.0.ffn_down.weight", "output.weight"]
+    total_bytes, secs = 0, 0.0
+    rng = np.random.default_rng(0)
+    for n in names:
+        t, dims, _, data = g.tensor(n)
+        k, rows = dims
+        x = rng.standard_normal(k).astype(np.float32)
+        t0 = time.perf_counter()
+        orc.gemv(t, data, rows, k, x, threads=1)
+        secs += time.perf_counter() - t0
+        total_bytes += data.size
+    g.close()
+    gbs = total_bytes / secs / 1e9
+    weight_bytes = info.weight_bytes - info.vocab * (info.hidden // 256) * 144
+    return {"value": round(1.0 / (weight_bytes / (gbs * 1e9)), 4), "unit": "tok/s (extrapolated)", "cores": 1,
+            "kind": "port", "gbs": round(gbs, 3),
+            "sample": f"oracle dequant+matvec of blk.0 (7 matrices) + output.weight, {total_bytes / 1e6:.0f} MB, "
+                      f"{secs:.1f} s single-threaded; tok/s = host GB/s / weight bytes per token"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--model", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is designed, not built "
+                                   "(see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import ribn_amd
+
+    cfg = dict(CFG)
+    if args.layers:
+        cfg["layers"] = args.layers
+    tmpdir = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    path = args.model or os.path.join(tmpdir, f"ribn_bench_qwen3_8b_q4km_{os.getpid()}.gguf")
+    made = False
+    t0 = time.time()
+    if not args.model:
+        ribn_amd.synth_qwen_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                                 ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                                 embd_type=ribn_amd.GGML_Q4_K, **cfg)
+        made = True
+    t_synth = time.time() - t0
+    try:
+        ctx = args.prompt + args.warmup + args.steps + 8
+        t0 = time.time()
+        m = ribn_amd.QwenRocm(path, context_tokens=ctx, max_sequences=1)
+        t_load = time.time() - t0
+        info = m.info
+        rng = np.random.default_rng(0)
+        prompt = rng.integers(0, info.vocab, args.prompt).tolist()
+        # warmup: captures every graph bucket the timed run uses
+        m.generate(prompt, args.warmup + args.steps + 1)
+        toks, tm = m.generate(prompt, args.steps + 1)
+        ms_per_step = tm.decode_ms / args.steps
+        decode_tps = 1000.0 / ms_per_step
+        prefill_tps = args.prompt / (tm.prefill_ms / 1000.0)
+        kern_ms, kern_bytes = m.bench_kernel(0, iters=100)
+        kern_gbs = kern_bytes / (kern_ms / 1e3) / 1e9
+        down_ms, down_bytes = m.bench_kernel(1, iters=100)
+        head_ms, head_bytes = m.bench_kernel(2, iters=20)
+        step_bytes, wbytes = algorithmic_bytes_per_token(info, args.prompt + args.steps / 2)
+        step_gbs = step_bytes / (ms_per_step / 1e3) / 1e9
+        m.close()
+        cpu = None if args.no_cpu else cpu_baseline(path, info)
+    finally:
+        if made and os.path.exists(path):
+            os.unlink(path)
+    out = {
+        "metric": "decode tok/s @bs1 Qwen3-8B-shape Q4_K_M; % HBM roofline; prefill tok/s",
+        "value": round(decode_tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights, fp16-staged activations, fp32 accumulate, bf16 KV",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to GGUF Q4_K_M; random prompt)",
+        "config": {"workload": "qwen3-8b-shape Q4_K_M bs1 greedy decode (BASELINE configs[2])",
+                   "prompt": args.prompt, "decode_tokens": args.steps, "layers": info.layers,
+                   "parallelism": "single GPU"},
+        "prefill_tok_s": round(prefill_tps, 2),
+        "prefill_path": "serial per-token graph replays (MFMA chunked prefill not yet built)",
+        "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "matvec_kernel (layer-0 ffn gate/up, Q4_K 4096->2x12288, SwiGLU epilogue)",
+                     "avg_us": round(kern_ms * 1e3, 2), "bytes_per_launch": int(kern_bytes)},
+        "kernels_us": {"gate_up_q4k": round(kern_ms * 1e3, 2), "down_q6k": round(down_ms * 1e3, 2),
+                       "down_gbs": round(down_bytes / down_ms / 1e6, 1), "head_q6k": round(head_ms * 1e3, 2),
+                       "head_gbs": round(head_bytes / head_ms / 1e6, 1)},
+        "cpu_baseline": cpu,
+        "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)},
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,210 @@
+/*
+ * librocm_ribn -- MI355X (gfx950) backend for ribn's autoregressive token loop.
+ *
+ * C ABI. Plain pointers and sizes only; every array argument is caller-owned
+ * host memory that the library never retains past the call (the reference's
+ * rule for borrowed batches, crates/runtime/src/executor.rs:213-215), unless
+ * a function says "device pointer".
+ *
+ * Status codes: RIBN_OK (0); RIBN_PENDING (1, poll only); negative = error.
+ * Every function that can fail takes (char *err, size_t err_len) and writes a
+ * NUL-terminated diagnostic of at most min(err_len, 4096) bytes
+ * (ExecutionError, executor.rs:134-152).
+ *
+ * Threading: one handle is used by one thread at a time (the reference trait
+ * is Send, not Sync; every method takes &mut self, executor.rs:171).
+ */
+#ifndef RIBN_ROCM_H
+#define RIBN_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RIBN_OK 0
+#define RIBN_PENDING 1
+#define RIBN_ERR_INVALID (-1)     /* bad argument / contract violation */
+#define RIBN_ERR_IO (-2)          /* file access */
+#define RIBN_ERR_FORMAT (-3)      /* GGUF parse / unsupported model */
+#define RIBN_ERR_DEVICE (-4)      /* HIP failure (the handle is faulted) */
+#define RIBN_ERR_FAULTED (-5)     /* handle faulted by an earlier error */
+#define RIBN_ERR_BUSY (-6)        /* a preparation or submission is outstanding */
+#define RIBN_ERR_CAPACITY (-7)    /* exceeds prepared limits */
+
+/* GGML value types accepted by the kernels (crates/gguf/src/lib.rs:508-535). */
+#define RIBN_GGML_F32 0
+#define RIBN_GGML_F16 1
+#define RIBN_GGML_Q8_0 8
+#define RIBN_GGML_Q4_K 12
+#define RIBN_GGML_Q6_K 14
+
+typedef struct ribn_rocm_model ribn_rocm_model;
+
+/* ------------------------------------------------------------------------ */
+/* Loading. Replaces QwenCuda::load_gguf (crates/qwen/src/cuda.rs:30) and
+ * loading::load (crates/qwen/src/loading.rs:93-190) with QwenLoadOptions
+ * (loading.rs:30-81). Accepts dense general.architecture qwen2 / qwen3 with
+ * Q8_0 / Q4_K / Q6_K matrices and F32 norms/biases. Unsupported architecture
+ * or value types are rejected with a message naming the field
+ * (the shape-generic counterpart of QwenCudaProfile::mismatch, profile.rs:70-142). */
+typedef struct {
+    uint32_t context_tokens;   /* per-sequence limit (0 -> min(GGUF context_length, 4096)) */
+    uint32_t max_sequences;    /* 0 -> 8 */
+    uint32_t max_batch_tokens; /* 0 -> 2048 */
+    uint32_t kv_pages;         /* 16-token BF16 pages in the pool (0 -> max_sequences*context/16) */
+    int32_t device;            /* HIP device ordinal */
+    uint32_t flags;            /* reserved, 0 */
+} ribn_rocm_load_options;
+
+int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
+                        char *err, size_t err_len);
+/* Synchronizes, then frees every device resource. Safe on NULL. */
+void ribn_rocm_free(ribn_rocm_model *model);
+
+/* ExecutorInfo + GenerationLimits (executor.rs:43-71). */
+typedef struct {
+    char name[128];
+    uint32_t context_tokens;
+    uint32_t max_sequences;
+    uint32_t max_batch_tokens;
+    uint32_t max_decode_tokens;
+    /* model geometry */
+    uint32_t hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, rope_dims;
+    uint64_t weight_bytes;     /* encoded bytes of all matrices on device */
+    uint64_t kv_bytes;         /* BF16 KV pool bytes */
+} ribn_rocm_info_t;
+int ribn_rocm_info(const ribn_rocm_model *model, ribn_rocm_info_t *out);
+
+/* ------------------------------------------------------------------------ */
+/* GenerationExecutor (crates/runtime/src/executor.rs:171-254). */
+#define RIBN_ADMIT_READY 0
+#define RIBN_ADMIT_REJECTED 1
+#define RIBN_ADMIT_DEFERRED 2
+#define RIBN_STEP_PREFILL 0
+#define RIBN_STEP_DECODE 1
+
+typedef struct {
+    uint32_t max_output_tokens;
+    float temperature;            /* only 0 (greedy) is accepted, as the reference */
+    const uint32_t *stop_tokens;
+    uint32_t n_stop_tokens;
+} ribn_rocm_token_options;
+
+/* BatchItem (executor.rs:75-85). */
+typedef struct {
+    uint64_t sequence;
+    uint32_t kind;                /* RIBN_STEP_PREFILL / RIBN_STEP_DECODE */
+    uint32_t prefix;
+    uint32_t token_budget;
+    uint32_t output_budget;
+} ribn_rocm_batch_item;
+
+/* StepCompletion (executor.rs:113-117); at most one sampled token per row. */
+typedef struct {
+    uint64_t sequence;
+    uint32_t prefix;
+    uint32_t n_tokens;            /* 0 or 1 */
+    uint32_t token;
+    uint32_t reserved;
+} ribn_rocm_step_completion;
+
+/* admit (executor.rs:186-191; Qwen rules crates/qwen/src/execution.rs:80-161).
+ * *admission receives RIBN_ADMIT_*; a rejection message goes to err. Returns
+ * RIBN_OK unless the owner faulted. */
+int ribn_rocm_admit(ribn_rocm_model *model, uint64_t request_id, uint64_t sequence,
+                    const uint32_t *tokens, uint32_t n_tokens, const ribn_rocm_token_options *options,
+                    int32_t *admission, char *err, size_t err_len);
+/* prepare (executor.rs:199). Every row accepted unchanged = BatchPreparation::Ready. */
+int ribn_rocm_prepare(ribn_rocm_model *model, const ribn_rocm_batch_item *items, size_t n_items,
+                      char *err, size_t err_len);
+/* abandon_preparation (executor.rs:206), idempotent. */
+int ribn_rocm_abandon(ribn_rocm_model *model, char *err, size_t err_len);
+/* submit (executor.rs:214): items must equal the prepared batch. */
+int ribn_rocm_submit(ribn_rocm_model *model, const ribn_rocm_batch_item *items, size_t n_items,
+                     uint64_t *submission, char *err, size_t err_len);
+/* poll (executor.rs:226): RIBN_OK and exactly n_items completions in batch
+ * order, RIBN_PENDING while device work is in flight, <0 on a terminal error. */
+int ribn_rocm_poll(ribn_rocm_model *model, uint64_t submission, ribn_rocm_step_completion *out,
+                   size_t out_cap, size_t *n_out, char *err, size_t err_len);
+/* release (executor.rs:236), idempotent after success. */
+int ribn_rocm_release(ribn_rocm_model *model, uint64_t sequence, char *err, size_t err_len);
+/* synchronize (executor.rs:245). */
+int ribn_rocm_synchronize(ribn_rocm_model *model, char *err, size_t err_len);
+
+/* ------------------------------------------------------------------------ */
+/* Lower seam: the per-sequence greedy step chain
+ * (CudaQwen35Decode::{prefill_step, decode_step, run_step}, nvidia/src/decode.rs:495-640,
+ * run_output_head decode.rs:686-700). The whole loop stays on the device: the
+ * argmax of step t is the input token of step t+1, and each step is one HIP
+ * graph replay. out_tokens receives n_new tokens. */
+typedef struct {
+    double prefill_ms;        /* device time, prompt */
+    double decode_ms;         /* device time, n_new-1 decode steps after the first token */
+    uint32_t prefill_tokens;
+    uint32_t decode_tokens;
+} ribn_rocm_timing;
+int ribn_rocm_generate(ribn_rocm_model *model, const uint32_t *prompt, uint32_t n_prompt,
+                       uint32_t n_new, uint32_t *out_tokens, ribn_rocm_timing *timing, char *err,
+                       size_t err_len);
+
+/* Teacher-forced trace for parity tests: runs tokens[0..n) one position at a
+ * time on a scratch sequence; for each position writes the argmax token, and
+ * optionally the final-normed logits (n*vocab floats) and the residual stream
+ * after the embedding and after every layer (n*(layers+1)*hidden floats). */
+int ribn_rocm_trace(ribn_rocm_model *model, const uint32_t *tokens, uint32_t n, uint32_t *argmax_out,
+                    float *logits_out, float *hidden_out, char *err, size_t err_len);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel-level entry points (tests and bench). Host buffers in and out; the
+ * weights go through the same load-time re-tiling as model tensors. */
+
+/* Device dequantization of `rows` rows of `k` elements, bit-exact with
+ * dequantize_block (crates/gguf/src/lib.rs:508-649). */
+int ribn_rocm_dequantize(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t k, float *out,
+                         char *err, size_t err_len);
+/* y = W x with the fused dequant-matvec kernel (gguf_gemv, nvidia/src/qwen_reference.rs:31-40;
+ * q*_gemv_warp, kernels/quantized/q4_k.cu:103, q6_k.cu:45, q8_0.cu:27). If rms_weight
+ * is not NULL the RMSNorm prologue is applied to x first (rms_norm, model_ops.rs:108). */
+int ribn_rocm_gemv(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t k, const float *x,
+                   const float *rms_weight, float eps, float *y, char *err, size_t err_len);
+/* Time `iters` launches of the matvec on device-resident data; *avg_ms gets the
+ * HIP-event average per launch (on the launch stream). */
+int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, uint32_t iters, double *avg_ms,
+                         char *err, size_t err_len);
+/* Greedy argmax (model_ops.rs:203-260): first maximum, NaN skipped. */
+int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, size_t err_len);
+
+/* Model-resident timing of the dominant decode kernel: replays the fused
+ * gate/up matvec of layer 0 `iters` times; *avg_ms per launch, *bytes the
+ * encoded weight bytes one launch streams. */
+int ribn_rocm_bench_model_kernel(ribn_rocm_model *model, uint32_t which, uint32_t iters, double *avg_ms,
+                                 uint64_t *bytes, char *err, size_t err_len);
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic model writer (test and benchmark inputs; no reference counterpart:
+ * the reference loads real artifacts only). Seeded N(0, weight_std) weights,
+ * quantized to GGML blocks, written as GGUF v3. */
+typedef struct {
+    int32_t qwen3;            /* 1: qwen3 (q/k norm, no bias); 0: qwen2 (q/k/v bias) */
+    uint32_t hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab;
+    uint32_t context_length;
+    float rope_base, rms_eps, weight_std;
+    float norm_jitter;        /* norm weights = 1 + N(0, norm_jitter) (0: exactly 1) */
+    uint64_t seed;
+    uint32_t weight_type;     /* default matrix type (0 -> Q4_K) */
+    uint32_t attn_v_type, ffn_down_type, output_type, embd_type; /* 0 -> weight_type */
+    int32_t tied_output;      /* 1: no output.weight (head tied to token_embd) */
+    int32_t threads;          /* 0 -> min(16, cores) */
+} ribn_rocm_synth_config;
+int ribn_rocm_synth_qwen_gguf(const char *path, const ribn_rocm_synth_config *config, char *err,
+                              size_t err_len);
+/* Quantize n floats into GGML blocks (n a multiple of the block size). */
+int ribn_rocm_quantize(uint32_t type, const float *x, uint64_t n, uint8_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

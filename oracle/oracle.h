@@ -1,0 +1,104 @@
+/*
+ * ribn-rocm CPU oracle -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's host arithmetic for the Qwen
+ * autoregressive token loop. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the timed CPU baseline). The product library never links it.
+ *
+ * Pinning status of each function (what checks it besides its own formula):
+ *   orc_f16_to_f32        pinned: reference KATs (lib.rs:1480-1497) + exhaustive
+ *                         65536-pattern comparison against IEEE binary16 (numpy)
+ *   orc_tensor_layout     pinned: byte_len KATs (lib.rs:1585-1625)
+ *   orc_dequantize_block  pinned: reference KATs (lib.rs:1480-1583), dyadic block
+ *                         builder identity (nvidia/tests/q4_q8_1.rs:15-50,205-228)
+ *   orc_gguf_*            pinned: parser fixture (lib.rs:1219-1276), error cases
+ *   orc_gemv_q            pinned: closed form (fp64 dot of dequantized values)
+ *   orc_rms_norm          pinned: constant-vector closed form
+ *   orc_rope_neox         pinned: pos 0 identity, norm preservation, pos-additivity
+ *   orc_argmax            pinned: ties -> lowest index, NaN skipped
+ *   orc_qwen_*            composition of the above; the reference cannot run dense
+ *                         Qwen2/Qwen3, so the composed forward is pinned only by
+ *                         its parts plus single-token closed forms (1-token
+ *                         attention returns v).
+ */
+#ifndef RIBN_ORACLE_H
+#define RIBN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes (mirror the GgufError variants the tests exercise). */
+enum {
+    ORC_OK = 0,
+    ORC_ERR_UNSUPPORTED_TYPE = -1,
+    ORC_ERR_BLOCK_LENGTH = -2,
+    ORC_ERR_MAGIC = -3,
+    ORC_ERR_VERSION = -4,
+    ORC_ERR_TRUNCATED = -5,
+    ORC_ERR_DUPLICATE_METADATA = -6,
+    ORC_ERR_ALIGNMENT = -7,
+    ORC_ERR_OFFSET = -8,
+    ORC_ERR_DIMENSION = -9,
+    ORC_ERR_IO = -10,
+    ORC_ERR_LENGTH = -11,
+    ORC_ERR_MISSING = -12,
+    ORC_ERR_CONFIG = -13,
+};
+
+float orc_f16_to_f32(uint16_t bits);
+int orc_tensor_layout(uint32_t value_type, uint64_t *block_elements, uint64_t *block_bytes);
+/* Dequantize exactly one block. Returns the number of values written or an error. */
+int orc_dequantize_block(uint32_t value_type, const uint8_t *encoded, size_t len, float *out);
+/* Dequantize `nblocks` consecutive blocks. Returns values written or an error. */
+int64_t orc_dequantize(uint32_t value_type, const uint8_t *encoded, size_t len, float *out);
+/* byte_len of a tensor with the given dims (ne0 first), or a negative error. */
+int64_t orc_tensor_byte_len(uint32_t value_type, const uint64_t *dims, uint32_t ndims);
+
+/* ---- GGUF v3 reader ---- */
+typedef struct orc_gguf orc_gguf;
+int orc_gguf_open(const char *path, orc_gguf **out);
+void orc_gguf_close(orc_gguf *g);
+uint32_t orc_gguf_version(const orc_gguf *g);
+uint64_t orc_gguf_tensor_count(const orc_gguf *g);
+uint64_t orc_gguf_data_offset(const orc_gguf *g);
+/* metadata accessors: return 0 on success, ORC_ERR_MISSING / ORC_ERR_CONFIG otherwise */
+int orc_gguf_get_u64(const orc_gguf *g, const char *key, uint64_t *out);
+int orc_gguf_get_f32(const orc_gguf *g, const char *key, float *out);
+int orc_gguf_get_str(const orc_gguf *g, const char *key, char *out, size_t cap);
+/* tensor lookup by name: fills type, dims (up to 4) and absolute byte range */
+int orc_gguf_tensor(const orc_gguf *g, const char *name, uint32_t *type, uint64_t *dims,
+                    uint32_t *ndims, uint64_t *start, uint64_t *len);
+const uint8_t *orc_gguf_bytes(const orc_gguf *g);
+
+/* ---- host equations ---- */
+/* y[n] = sum_k dequant(W[n,k]) * x[k], block-streamed dequant then an f32
+ * sequential dot per row (gguf_gemv, qwen_reference.rs:31-40). */
+int orc_gemv_q(uint32_t value_type, const uint8_t *w, uint64_t rows, uint64_t k,
+               const float *x, float *y, int threads);
+void orc_rms_norm(const float *x, const float *w, float *y, int n, float eps);
+void orc_rope_neox(float *v, int heads, int head_dim, int rot_dim, int64_t pos, float base);
+uint32_t orc_argmax(const float *logits, int n);
+
+/* ---- dense Qwen2/Qwen3 FP32 forward (composition) ---- */
+typedef struct orc_qwen orc_qwen;
+int orc_qwen_open(const char *gguf_path, int max_ctx, orc_qwen **out);
+void orc_qwen_close(orc_qwen *m);
+/* config: hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, rot_dim */
+void orc_qwen_config(const orc_qwen *m, int32_t *cfg8, float *eps, float *rope_base);
+/* Run one token at position `pos` (positions must be fed in order 0,1,2...).
+ * logits (vocab floats) may be NULL; hidden_trace, if not NULL, receives
+ * (layers+1)*hidden floats: the residual stream after embedding and after each
+ * layer. final_norm (hidden floats) may be NULL. */
+int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *hidden_trace,
+                  float *final_norm);
+void orc_qwen_reset(orc_qwen *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

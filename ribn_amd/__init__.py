@@ -1,0 +1,359 @@
+"""ribn_amd: Python binding of librocm_ribn (the MI355X backend of ribn's token loop).
+
+The product is the C ABI in ``include/ribn_rocm.h`` (C++/HIP, built in-tree as
+``ribn_amd/librocm_ribn.so``). This module is a thin ctypes mirror of it, shaped
+like the reference's Rust surfaces so tests read like the reference's own:
+
+* :class:`QwenRocm` - ``GenerationExecutor`` (crates/runtime/src/executor.rs:171-254)
+  with ``admit / prepare / abandon_preparation / submit / poll / release /
+  synchronize``, plus the device-resident greedy loop (``generate``) and a
+  teacher-forced ``trace``.
+* kernel-level helpers: ``dequantize`` (dequantize_block, crates/gguf/src/lib.rs:508),
+  ``gemv`` (gguf_gemv, crates/nvidia/src/qwen_reference.rs:31), ``argmax``
+  (model_ops.rs:203).
+
+There is no CPU fallback: importing fails loudly when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librocm_ribn.so")
+
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 8, 12, 14
+BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
+
+RIBN_OK, RIBN_PENDING = 0, 1
+ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
+STEP_PREFILL, STEP_DECODE = 0, 1
+
+
+class RibnError(RuntimeError):
+    """An error status from librocm_ribn (ExecutionError)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+        "(there is no CPU fallback)"
+    )
+_lib = ctypes.CDLL(LIB_PATH)
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_ERR = 4096
+
+
+class LoadOptions(ctypes.Structure):
+    _fields_ = [("context_tokens", ctypes.c_uint32), ("max_sequences", ctypes.c_uint32),
+                ("max_batch_tokens", ctypes.c_uint32), ("kv_pages", ctypes.c_uint32),
+                ("device", ctypes.c_int32), ("flags", ctypes.c_uint32)]
+
+
+class Info(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("context_tokens", ctypes.c_uint32),
+                ("max_sequences", ctypes.c_uint32), ("max_batch_tokens", ctypes.c_uint32),
+                ("max_decode_tokens", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
+                ("layers", ctypes.c_uint32), ("q_heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
+                ("rope_dims", ctypes.c_uint32), ("weight_bytes", ctypes.c_uint64), ("kv_bytes", ctypes.c_uint64)]
+
+
+class TokenOptions(ctypes.Structure):
+    _fields_ = [("max_output_tokens", ctypes.c_uint32), ("temperature", ctypes.c_float),
+                ("stop_tokens", _u32p), ("n_stop_tokens", ctypes.c_uint32)]
+
+
+class BatchItemC(ctypes.Structure):
+    _fields_ = [("sequence", ctypes.c_uint64), ("kind", ctypes.c_uint32), ("prefix", ctypes.c_uint32),
+                ("token_budget", ctypes.c_uint32), ("output_budget", ctypes.c_uint32)]
+
+
+class StepCompletionC(ctypes.Structure):
+    _fields_ = [("sequence", ctypes.c_uint64), ("prefix", ctypes.c_uint32), ("n_tokens", ctypes.c_uint32),
+                ("token", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class Timing(ctypes.Structure):
+    _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double),
+                ("prefill_tokens", ctypes.c_uint32), ("decode_tokens", ctypes.c_uint32)]
+
+
+class SynthConfig(ctypes.Structure):
+    _fields_ = [("qwen3", ctypes.c_int32), ("hidden", ctypes.c_uint32), ("layers", ctypes.c_uint32),
+                ("q_heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32), ("context_length", ctypes.c_uint32),
+                ("rope_base", ctypes.c_float), ("rms_eps", ctypes.c_float), ("weight_std", ctypes.c_float),
+                ("norm_jitter", ctypes.c_float), ("seed", ctypes.c_uint64), ("weight_type", ctypes.c_uint32),
+                ("attn_v_type", ctypes.c_uint32), ("ffn_down_type", ctypes.c_uint32),
+                ("output_type", ctypes.c_uint32), ("embd_type", ctypes.c_uint32),
+                ("tied_output", ctypes.c_int32), ("threads", ctypes.c_int32)]
+
+
+def _sig(name, res, *args):
+    f = getattr(_lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+_c = ctypes
+_sig("ribn_rocm_load_gguf", _c.c_int, _c.c_char_p, _c.POINTER(LoadOptions), _c.POINTER(_c.c_void_p), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_free", None, _c.c_void_p)
+_sig("ribn_rocm_info", _c.c_int, _c.c_void_p, _c.POINTER(Info))
+_sig("ribn_rocm_admit", _c.c_int, _c.c_void_p, _c.c_uint64, _c.c_uint64, _u32p, _c.c_uint32,
+     _c.POINTER(TokenOptions), _c.POINTER(_c.c_int32), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_prepare", _c.c_int, _c.c_void_p, _c.POINTER(BatchItemC), _c.c_size_t, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_abandon", _c.c_int, _c.c_void_p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_submit", _c.c_int, _c.c_void_p, _c.POINTER(BatchItemC), _c.c_size_t, _c.POINTER(_c.c_uint64),
+     _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_poll", _c.c_int, _c.c_void_p, _c.c_uint64, _c.POINTER(StepCompletionC), _c.c_size_t,
+     _c.POINTER(_c.c_size_t), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_release", _c.c_int, _c.c_void_p, _c.c_uint64, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_synchronize", _c.c_int, _c.c_void_p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_generate", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _c.c_uint32, _u32p, _c.POINTER(Timing),
+     _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_trace", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _u32p, _f32p, _f32p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_dequantize", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemv", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _f32p, _c.c_float, _f32p,
+     _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_bench_gemv", _c.c_int, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_uint32, _c.POINTER(_c.c_double),
+     _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_argmax", _c.c_int, _f32p, _c.c_uint64, _u32p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_bench_model_kernel", _c.c_int, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.POINTER(_c.c_double),
+     _c.POINTER(_c.c_uint64), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_synth_qwen_gguf", _c.c_int, _c.c_char_p, _c.POINTER(SynthConfig), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_quantize", _c.c_int, _c.c_uint32, _f32p, _c.c_uint64, _u8p)
+
+
+def _ptr(a: np.ndarray, t):
+    return a.ctypes.data_as(t)
+
+
+def _check(rc: int, buf) -> int:
+    if rc < 0:
+        raise RibnError(rc, buf.value.decode(errors="replace"))
+    return rc
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+# --------------------------------------------------------------------------
+# synthetic models and kernel-level helpers
+
+def synth_qwen_gguf(path: str, *, qwen3: bool = True, hidden: int, layers: int, q_heads: int, kv_heads: int,
+                    head_dim: int, ffn: int, vocab: int, weight_type: int = GGML_Q4_K, attn_v_type: int = 0,
+                    ffn_down_type: int = 0, output_type: int = 0, embd_type: int = 0, rope_base: float = 1e6,
+                    rms_eps: float = 1e-6, weight_std: float = 0.02, norm_jitter: float = 0.0, seed: int = 0,
+                    context_length: int = 32768, tied_output: bool = False, threads: int = 0) -> str:
+    """Write a seeded synthetic dense-Qwen GGUF v3 (N(0, weight_std) weights, GGML-quantized)."""
+    cfg = SynthConfig(int(qwen3), hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, context_length,
+                      rope_base, rms_eps, weight_std, norm_jitter, seed, weight_type, attn_v_type, ffn_down_type,
+                      output_type, embd_type, int(tied_output), threads)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_synth_qwen_gguf(path.encode(), ctypes.byref(cfg), err, _ERR), err)
+    return path
+
+
+def quantize(type_: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    be, bb = BLOCK[type_]
+    if x.size % be:
+        raise ValueError("size is not a multiple of the block size")
+    out = np.zeros(x.size // be * bb, dtype=np.uint8)
+    if _lib.ribn_rocm_quantize(type_, _ptr(x, _f32p), x.size, _ptr(out, _u8p)) != 0:
+        raise RibnError(-1, "quantize failed")
+    return out
+
+
+def dequantize(type_: int, blocks: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Device dequantization (bit-exact with dequantize_block)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(rows * k, dtype=np.float32)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_dequantize(type_, _ptr(blocks, _u8p), rows, k, _ptr(out, _f32p), err, _ERR), err)
+    return out.reshape(rows, k)
+
+
+def gemv(type_: int, blocks: np.ndarray, rows: int, k: int, x: np.ndarray, rms_weight: Optional[np.ndarray] = None,
+         eps: float = 1e-6) -> np.ndarray:
+    """Fused dequant-matvec on the device: y = W x (optionally W rms_norm(x) * w)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(rows, dtype=np.float32)
+    w = None if rms_weight is None else np.ascontiguousarray(rms_weight, dtype=np.float32)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_gemv(type_, _ptr(blocks, _u8p), rows, k, _ptr(x, _f32p),
+                               None if w is None else _ptr(w, _f32p), eps, _ptr(y, _f32p), err, _ERR), err)
+    return y
+
+
+def bench_gemv(type_: int, rows: int, k: int, iters: int = 50) -> float:
+    """Average device milliseconds per matvec launch (HIP events)."""
+    ms = ctypes.c_double()
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_bench_gemv(type_, rows, k, iters, ctypes.byref(ms), err, _ERR), err)
+    return ms.value
+
+
+def argmax(logits: np.ndarray) -> int:
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    out = ctypes.c_uint32()
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_argmax(_ptr(logits, _f32p), logits.size, ctypes.byref(out), err, _ERR), err)
+    return out.value
+
+
+# --------------------------------------------------------------------------
+# GenerationExecutor mirror
+
+@dataclass(frozen=True)
+class BatchItem:
+    """BatchItem (executor.rs:75-85)."""
+    sequence: int
+    kind: int
+    prefix: int
+    token_budget: int
+    output_budget: int
+
+
+@dataclass(frozen=True)
+class StepCompletion:
+    """StepCompletion (executor.rs:113-117)."""
+    sequence: int
+    prefix: int
+    tokens: tuple
+
+
+@dataclass(frozen=True)
+class Admission:
+    kind: int          # ADMIT_READY / ADMIT_REJECTED / ADMIT_DEFERRED
+    message: str = ""
+
+
+def _items(batch: Sequence[BatchItem]):
+    arr = (BatchItemC * max(1, len(batch)))()
+    for i, b in enumerate(batch):
+        arr[i] = BatchItemC(b.sequence, b.kind, b.prefix, b.token_budget, b.output_budget)
+    return arr
+
+
+class QwenRocm:
+    """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
+
+    def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
+                 kv_pages: int = 0, device: int = 0):
+        opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device, 0)
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERR)
+        _check(_lib.ribn_rocm_load_gguf(path.encode(), ctypes.byref(opts), ctypes.byref(h), err, _ERR), err)
+        self._h = h
+        info = Info()
+        _lib.ribn_rocm_info(self._h, ctypes.byref(info))
+        self.info = info
+
+    # lifecycle
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.ribn_rocm_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _call(self, fn, *args):
+        err = ctypes.create_string_buffer(_ERR)
+        rc = fn(self._h, *args, err, _ERR)
+        return _check(rc, err), err.value.decode(errors="replace")
+
+    # executor contract
+    def admit(self, request_id: int, sequence: int, tokens: Sequence[int], max_output_tokens: int,
+              temperature: float = 0.0, stop_tokens: Sequence[int] = ()) -> Admission:
+        toks = _u32(tokens)
+        stops = _u32(stop_tokens) if len(stop_tokens) else np.zeros(1, np.uint32)
+        opt = TokenOptions(max_output_tokens, temperature, _ptr(stops, _u32p), len(stop_tokens))
+        kind = ctypes.c_int32(-1)
+        _, msg = self._call(_lib.ribn_rocm_admit, request_id, sequence, _ptr(toks, _u32p) if toks.size else None,
+                            toks.size, ctypes.byref(opt), ctypes.byref(kind))
+        return Admission(kind.value, msg if kind.value != ADMIT_READY else "")
+
+    def prepare(self, batch: Sequence[BatchItem]) -> None:
+        self._call(_lib.ribn_rocm_prepare, _items(batch), len(batch))
+
+    def abandon_preparation(self) -> None:
+        self._call(_lib.ribn_rocm_abandon)
+
+    def submit(self, batch: Sequence[BatchItem]) -> int:
+        sid = ctypes.c_uint64()
+        self._call(_lib.ribn_rocm_submit, _items(batch), len(batch), ctypes.byref(sid))
+        return sid.value
+
+    def poll(self, submission: int):
+        cap = max(1, self.info.max_sequences)
+        out = (StepCompletionC * cap)()
+        n = ctypes.c_size_t()
+        rc, _ = self._call(_lib.ribn_rocm_poll, submission, out, cap, ctypes.byref(n))
+        if rc == RIBN_PENDING:
+            return None
+        return [StepCompletion(out[i].sequence, out[i].prefix, (out[i].token,) if out[i].n_tokens else ())
+                for i in range(n.value)]
+
+    def release(self, sequence: int) -> None:
+        self._call(_lib.ribn_rocm_release, sequence)
+
+    def synchronize(self) -> None:
+        self._call(_lib.ribn_rocm_synchronize)
+
+    # lower seams
+    def generate(self, prompt: Sequence[int], n_new: int):
+        p = _u32(prompt)
+        out = np.zeros(n_new, dtype=np.uint32)
+        t = Timing()
+        self._call(_lib.ribn_rocm_generate, _ptr(p, _u32p), p.size, n_new, _ptr(out, _u32p), ctypes.byref(t))
+        return out, t
+
+    def trace(self, tokens: Sequence[int], logits: bool = True, hidden: bool = False):
+        t = _u32(tokens)
+        n = t.size
+        am = np.zeros(n, dtype=np.uint32)
+        lg = np.zeros((n, self.info.vocab), dtype=np.float32) if logits else None
+        hd = np.zeros((n, self.info.layers + 1, self.info.hidden), dtype=np.float32) if hidden else None
+        self._call(_lib.ribn_rocm_trace, _ptr(t, _u32p), n, _ptr(am, _u32p),
+                   None if lg is None else _ptr(lg, _f32p), None if hd is None else _ptr(hd, _f32p))
+        return am, lg, hd
+
+    def bench_kernel(self, which: int, iters: int = 50):
+        ms = ctypes.c_double()
+        nbytes = ctypes.c_uint64()
+        self._call(_lib.ribn_rocm_bench_model_kernel, which, iters, ctypes.byref(ms), ctypes.byref(nbytes))
+        return ms.value, nbytes.value
+
+
+__all__ = [
+    "QwenRocm", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
+    "dequantize", "gemv", "bench_gemv", "argmax", "LIB_PATH", "GGML_F32", "GGML_F16", "GGML_Q8_0", "GGML_Q4_K",
+    "GGML_Q6_K", "BLOCK", "STEP_PREFILL", "STEP_DECODE", "ADMIT_READY", "ADMIT_REJECTED", "ADMIT_DEFERRED",
+]

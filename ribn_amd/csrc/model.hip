@@ -1,0 +1,1111 @@
+// librocm_ribn host side: GGUF loading with weight re-tiling, the per-token
+// launch chain captured in HIP graphs, the device-resident greedy loop, and
+// the GenerationExecutor-shaped C ABI (include/ribn_rocm.h).
+//
+// Reference counterparts: loading::load (crates/qwen/src/loading.rs:93-190),
+// CudaQwen35Weights::stage (nvidia/src/staging.rs:263), CudaQwen35Decode::run_step
+// (nvidia/src/decode.rs:550-640), QwenExecution admit/prepare/submit/poll/commit
+// (crates/qwen/src/execution.rs:80-414).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <map>
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/ribn_rocm.h"
+#include "common.h"
+#include "gguf.h"
+#include "kernels.h"
+
+using namespace ribn;
+
+namespace {
+
+struct Layer {
+    QMat q, k, v, o, gate, up, down;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    float *q_bias = nullptr, *k_bias = nullptr, *v_bias = nullptr;
+    uint16_t *kc = nullptr, *vc = nullptr;
+};
+
+struct Sequence {
+    int slot = -1;
+    uint32_t prompt_len = 0;
+    uint32_t committed = 0;   // logical prefix
+    bool has_next = false;
+    uint32_t next = 0;
+    bool in_flight = false;
+    std::vector<int32_t> pages;
+};
+
+struct Submission {
+    uint64_t id = 0;
+    std::vector<ribn_rocm_batch_item> items;
+    hipEvent_t done = nullptr;
+};
+
+int splits_for_ctx(int ctx) {
+    int want = (ctx + 31) / 32;
+    int s = 1;
+    while (s < want && s < kMaxSplits) s <<= 1;
+    return s;
+}
+
+std::string hip_msg(const char* what, hipError_t e) {
+    return std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+}
+
+}  // namespace
+
+struct ribn_rocm_model {
+    // geometry
+    int H = 0, L = 0, hq = 0, hkv = 0, hd = 0, F = 0, V = 0, rot = 0;
+    float eps = 1e-6f, base = 1e6f;
+    bool qwen3 = false;
+    std::string name;
+    uint32_t context = 0, max_seqs = 0, max_batch_tokens = 0, kv_pages = 0;
+    int max_pages = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void*> dev_allocs;
+    std::vector<void*> host_allocs;
+    uint64_t weight_bytes = 0, kv_bytes = 0;
+
+    QMat embd{}, out{};
+    float* out_norm = nullptr;
+    std::vector<Layer> layers;
+
+    // activations / scratch
+    float *h = nullptr, *raw = nullptr, *qbuf = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+    float* part = nullptr;
+    uint32_t* counters = nullptr;   // [hq + hkv] qkv, [hkv] attention, [1] head
+    uint64_t* head_partial = nullptr;
+    int head_wgs = 0;
+
+    // sequence slots (max_seqs + 1; the last one is the scratch slot of generate/trace)
+    SeqState* d_slots = nullptr;
+    int32_t* d_pages = nullptr;
+    uint32_t* d_tokens = nullptr;
+    StepCtl* d_ctl = nullptr;
+    SeqState** h_slot_ptr = nullptr;   // pinned: &d_slots[i]
+    SeqState* h_state = nullptr;        // pinned mirrors
+    int32_t* h_pages = nullptr;
+    uint32_t* h_tokens = nullptr;
+    uint32_t* h_out = nullptr;          // pinned sampled tokens per submitted row
+    std::vector<int> free_slots;
+    std::vector<int32_t> free_pages;
+
+    std::vector<MvArgs> mv_qkv, mv_o, mv_gu, mv_down;
+    std::vector<int> wg_qkv, wg_o, wg_gu, wg_down;
+    MvArgs mv_head{};
+    std::map<int, hipGraphExec_t> graphs;   // key: n_splits * 2 + head
+
+    // executor state
+    std::map<uint64_t, Sequence> seqs;
+    bool faulted = false;
+    bool has_prepared = false;
+    std::vector<ribn_rocm_batch_item> prepared;
+    bool has_pending = false;
+    Submission pending;
+    uint64_t next_submission = 1;
+};
+
+namespace {
+
+int fail(ribn_rocm_model* M, char* err, size_t err_len, const std::string& msg, int code = RIBN_ERR_DEVICE) {
+    if (M && code == RIBN_ERR_DEVICE) M->faulted = true;
+    set_err(err, err_len, msg);
+    return code;
+}
+
+#define HIPCHK(expr)                                                             \
+    do {                                                                         \
+        hipError_t e_ = (expr);                                                  \
+        if (e_ != hipSuccess) return fail(M, err, err_len, hip_msg(#expr, e_)); \
+    } while (0)
+
+template <typename T>
+hipError_t dalloc(ribn_rocm_model* M, T** p, size_t bytes) {
+    void* v = nullptr;
+    hipError_t e = hipMalloc(&v, bytes ? bytes : 256);
+    if (e == hipSuccess) {
+        M->dev_allocs.push_back(v);
+        *p = static_cast<T*>(v);
+    }
+    return e;
+}
+template <typename T>
+hipError_t halloc(ribn_rocm_model* M, T** p, size_t bytes) {
+    void* v = nullptr;
+    hipError_t e = hipHostMalloc(&v, bytes ? bytes : 256, hipHostMallocDefault);
+    if (e == hipSuccess) {
+        M->host_allocs.push_back(v);
+        *p = static_cast<T*>(v);
+    }
+    return e;
+}
+
+// Split GGUF blocks into the device planes described in kernels.h (QMat).
+void retile(uint32_t type, const uint8_t* src, uint64_t n_blocks, uint8_t* a, uint8_t* b, uint8_t* c, uint8_t* d) {
+    auto work = [&](uint64_t b0, uint64_t b1) {
+        for (uint64_t i = b0; i < b1; i++) {
+            if (type == GGML_Q4_K) {
+                const uint8_t* s = src + i * 144;
+                std::memcpy(b + i * 16, s, 16);
+                std::memcpy(a + i * 128, s + 16, 128);
+            } else if (type == GGML_Q6_K) {
+                const uint8_t* s = src + i * 210;
+                std::memcpy(a + i * 128, s, 128);
+                std::memcpy(b + i * 64, s + 128, 64);
+                std::memcpy(c + i * 16, s + 192, 16);
+                std::memcpy(d + i * 2, s + 208, 2);
+            } else {
+                const uint8_t* s = src + i * 34;
+                std::memcpy(b + i * 2, s, 2);
+                std::memcpy(a + i * 32, s + 2, 32);
+            }
+        }
+    };
+    int nt = (int)std::min<uint64_t>(16, std::max<uint64_t>(1, n_blocks / 65536));
+    if (nt <= 1) { work(0, n_blocks); return; }
+    std::vector<std::thread> th;
+    uint64_t per = (n_blocks + nt - 1) / nt;
+    for (int t = 0; t < nt; t++) th.emplace_back(work, std::min(n_blocks, per * t), std::min(n_blocks, per * (t + 1)));
+    for (auto& x : th) x.join();
+}
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Plane sizes for a [rows][k] matrix of `type`.
+void plane_sizes(uint32_t type, uint64_t nblocks, size_t* sa, size_t* sb, size_t* sc, size_t* sd) {
+    *sa = *sb = *sc = *sd = 0;
+    if (type == GGML_Q4_K) { *sa = nblocks * 128; *sb = nblocks * 16; }
+    else if (type == GGML_Q6_K) { *sa = nblocks * 128; *sb = nblocks * 64; *sc = nblocks * 16; *sd = nblocks * 2; }
+    else { *sa = nblocks * 32; *sb = nblocks * 2; }
+}
+
+// Allocate planes and upload re-tiled blocks. `blocks` may be host memory of
+// exactly rows*k/block_elems GGUF blocks.
+hipError_t upload_qmat(ribn_rocm_model* M, uint32_t type, uint64_t rows, uint64_t k, const uint8_t* blocks, QMat* out,
+                       std::vector<uint8_t>& staging) {
+    uint64_t be, bb;
+    type_layout(type, &be, &bb);
+    const uint64_t nblocks = rows * (k / be);
+    size_t sa, sb, sc, sd;
+    plane_sizes(type, nblocks, &sa, &sb, &sc, &sd);
+    const size_t total = align256(sa) + align256(sb) + align256(sc) + align256(sd);
+    uint8_t* dev = nullptr;
+    hipError_t e = dalloc(M, &dev, total);
+    if (e != hipSuccess) return e;
+    staging.resize(total);
+    uint8_t* ha = staging.data();
+    uint8_t* hb = ha + align256(sa);
+    uint8_t* hc = hb + align256(sb);
+    uint8_t* hdp = hc + align256(sc);
+    retile(type, blocks, nblocks, ha, hb, hc, hdp);
+    e = hipMemcpy(dev, staging.data(), total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+    QMat q{};
+    q.type = type;
+    q.rows = (uint32_t)rows;
+    q.k = (uint32_t)k;
+    q.nb = (uint32_t)(k / be);
+    q.a = dev;
+    q.b = dev + (hb - ha);
+    q.c = dev + (hc - ha);
+    q.d = dev + (hdp - ha);
+    *out = q;
+    M->weight_bytes += nblocks * bb;
+    return hipSuccess;
+}
+
+// Items per wave for a launch of `items` two-row items: the largest power of two
+// (<= cap) that still leaves >= 2048 workgroups of 4 waves.
+int choose_ipw(int items, int cap) {
+    int ipw = 1;
+    while (ipw < cap && items / (4 * ipw * 2) >= 2048) ipw *= 2;
+    return ipw;
+}
+
+}  // namespace
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Per-launch argument blocks, built once at load (only positions, page tables
+// and tokens change between steps, and those live in device memory).
+MvArgs mv_base(const float* x, const float* norm_w, float eps, int k, int mode, const StepCtl* ctl) {
+    MvArgs a{};
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.k = k;
+    a.mode = mode;
+    a.ctl = ctl;
+    return a;
+}
+
+// Assign workgroups to segments; returns the grid size.
+int layout_segments(MvArgs& a) {
+    const int rpw = matvec_rows_per_wg(a);
+    int wg = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].wg_begin = wg;
+        wg += ((int)a.seg[i].w.rows + rpw - 1) / rpw;
+    }
+    return wg;
+}
+
+void build_launches(ribn_rocm_model* M) {
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    M->mv_qkv.clear(); M->mv_o.clear(); M->mv_gu.clear(); M->mv_down.clear();
+    M->wg_qkv.clear(); M->wg_o.clear(); M->wg_gu.clear(); M->wg_down.clear();
+    for (int l = 0; l < M->L; l++) {
+        Layer& y = M->layers[l];
+        MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_QKV, M->d_ctl);
+        q.items_per_wave = 1;   // 8 rows per workgroup: divides every head_dim
+        q.nseg = 3;
+        q.seg[0].w = y.q; q.seg[0].out = M->raw; q.seg[0].bias = y.q_bias; q.seg[0].kind = 0;
+        q.seg[1].w = y.k; q.seg[1].out = M->raw + qd; q.seg[1].bias = y.k_bias; q.seg[1].kind = 1;
+        q.seg[2].w = y.v; q.seg[2].out = M->raw + qd + kd; q.seg[2].bias = y.v_bias; q.seg[2].kind = 2;
+        q.qkv.raw = M->raw;
+        q.qkv.q_out = M->qbuf;
+        q.qkv.kcache = y.kc;
+        q.qkv.vcache = y.vc;
+        q.qkv.q_norm = y.q_norm;
+        q.qkv.k_norm = y.k_norm;
+        q.qkv.counters = M->counters;
+        q.qkv.hq = M->hq; q.qkv.hkv = M->hkv; q.qkv.hd = M->hd; q.qkv.rot = M->rot;
+        q.qkv.rope_base = M->base; q.qkv.eps = M->eps;
+        M->wg_qkv.push_back(layout_segments(q));
+        M->mv_qkv.push_back(q);
+
+        MvArgs o = mv_base(M->attn, nullptr, 0.f, qd, MV_ADD, M->d_ctl);
+        o.nseg = 1;
+        o.seg[0].w = y.o; o.seg[0].out = M->h;
+        o.items_per_wave = choose_ipw(M->H / 2, 4);
+        M->wg_o.push_back(layout_segments(o));
+        M->mv_o.push_back(o);
+
+        MvArgs g = mv_base(M->h, y.ffn_norm, M->eps, M->H, MV_SILU, M->d_ctl);
+        g.nseg = 1;
+        g.seg[0].w = y.gate; g.seg[0].w2 = y.up; g.seg[0].out = M->act;
+        g.items_per_wave = choose_ipw(M->F, 4);
+        M->wg_gu.push_back(layout_segments(g));
+        M->mv_gu.push_back(g);
+
+        MvArgs d = mv_base(M->act, nullptr, 0.f, M->F, MV_ADD, M->d_ctl);
+        d.nseg = 1;
+        d.seg[0].w = y.down; d.seg[0].out = M->h;
+        d.items_per_wave = choose_ipw(M->H / 2, 4);
+        M->wg_down.push_back(layout_segments(d));
+        M->mv_down.push_back(d);
+    }
+    MvArgs hdv = mv_base(M->h, M->out_norm, M->eps, M->H, MV_HEAD, M->d_ctl);
+    hdv.nseg = 1;
+    hdv.seg[0].w = M->out; hdv.seg[0].out = M->logits;
+    hdv.items_per_wave = choose_ipw(M->V / 2, 8);
+    hdv.head.partial = M->head_partial;
+    hdv.head.counter = M->counters + M->hq + 2 * M->hkv;
+    M->head_wgs = layout_segments(hdv);
+    M->mv_head = hdv;
+}
+
+// One step of the token loop for the active sequence (decode.rs:550-640):
+// embedding -> L x [QKV(+norm,+rope,+KV append) -> attention -> O(+residual)
+// -> gate/up(+norm,+SwiGLU) -> down(+residual)] -> head(+norm,+argmax) or advance.
+hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trace) {
+    hipStream_t st = M->stream;
+    hipError_t e = launch_embed(M->embd, M->H, M->h, M->d_ctl, st);
+    if (e != hipSuccess) return e;
+    if (trace && (e = hipMemcpyAsync(trace, M->h, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
+        return e;
+    AttnArgs at{};
+    at.q = M->qbuf;
+    at.part = M->part;
+    at.counters = M->counters + M->hq + M->hkv;
+    at.out = M->attn;
+    at.ctl = M->d_ctl;
+    at.hq = M->hq; at.hkv = M->hkv; at.hd = M->hd; at.n_splits = n_splits;
+    at.scale_log2 = 1.4426950408889634f / std::sqrt((float)M->hd);
+    for (int l = 0; l < M->L; l++) {
+        if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
+        at.kcache = M->layers[l].kc;
+        at.vcache = M->layers[l].vc;
+        if ((e = launch_attention(at, st)) != hipSuccess) return e;
+        if ((e = launch_matvec(M->mv_o[l], M->wg_o[l], st)) != hipSuccess) return e;
+        if ((e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st)) != hipSuccess) return e;
+        if ((e = launch_matvec(M->mv_down[l], M->wg_down[l], st)) != hipSuccess) return e;
+        if (trace &&
+            (e = hipMemcpyAsync(trace + (size_t)(l + 1) * M->H, M->h, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st)) !=
+                hipSuccess)
+            return e;
+    }
+    if (head) return launch_matvec(M->mv_head, M->head_wgs, st);
+    return launch_advance(M->d_ctl, st);
+}
+
+hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
+    const int ns = splits_for_ctx(ctx);
+    const int key = ns * 2 + (head ? 1 : 0);
+    auto it = M->graphs.find(key);
+    if (it == M->graphs.end()) {
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return e;
+        hipError_t e2 = enqueue_step(M, head, ns, nullptr);
+        e = hipStreamEndCapture(M->stream, &g);
+        if (e2 != hipSuccess) { if (g) hipGraphDestroy(g); return e2; }
+        if (e != hipSuccess) return e;
+        hipGraphExec_t ex = nullptr;
+        e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) return e;
+        it = M->graphs.emplace(key, ex).first;
+    }
+    return hipGraphLaunch(it->second, M->stream);
+}
+
+// Point the graphs at `slot` and (re)write its device state from the pinned mirror.
+hipError_t select_slot(ribn_rocm_model* M, int slot) {
+    return hipMemcpyAsync(M->d_ctl, &M->h_slot_ptr[slot], sizeof(SeqState*), hipMemcpyHostToDevice, M->stream);
+}
+
+hipError_t reset_slot(ribn_rocm_model* M, int slot, const std::vector<int32_t>& pages, const uint32_t* toks,
+                      uint32_t n_toks) {
+    SeqState& s = M->h_state[slot];
+    s.pos = 0;
+    s.last_token = 0;
+    int32_t* hp = M->h_pages + (size_t)slot * M->max_pages;
+    for (int i = 0; i < M->max_pages; i++) hp[i] = i < (int)pages.size() ? pages[i] : pages.empty() ? 0 : pages[0];
+    uint32_t* ht = M->h_tokens + (size_t)slot * (M->context + 1);
+    std::memcpy(ht, toks, sizeof(uint32_t) * n_toks);
+    hipError_t e = hipMemcpyAsync(M->d_pages + (size_t)slot * M->max_pages, hp, sizeof(int32_t) * M->max_pages,
+                                  hipMemcpyHostToDevice, M->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(M->d_tokens + (size_t)slot * (M->context + 1), ht, sizeof(uint32_t) * n_toks,
+                           hipMemcpyHostToDevice, M->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(&M->d_slots[slot], &s, sizeof(SeqState), hipMemcpyHostToDevice, M->stream);
+    return e;
+}
+
+bool take_pages(ribn_rocm_model* M, uint32_t tokens, std::vector<int32_t>* out) {
+    const size_t need = (tokens + kPageTokens - 1) / kPageTokens;
+    if (M->free_pages.size() < need) return false;
+    out->assign(M->free_pages.end() - need, M->free_pages.end());
+    M->free_pages.resize(M->free_pages.size() - need);
+    return true;
+}
+void give_pages(ribn_rocm_model* M, std::vector<int32_t>& pages) {
+    M->free_pages.insert(M->free_pages.end(), pages.begin(), pages.end());
+    pages.clear();
+}
+
+std::string validate_type(const GgufTensor* t, const char* what, bool matrix) {
+    if (!t) return std::string("missing tensor ") + what;
+    if (matrix) {
+        if (t->type != GGML_Q4_K && t->type != GGML_Q6_K && t->type != GGML_Q8_0)
+            return "tensor " + t->name + " has unsupported value type " + std::to_string(t->type) + " (" +
+                   type_name(t->type) + "); supported: Q4_K, Q6_K, Q8_0";
+    } else if (t->type != GGML_F32) {
+        return "tensor " + t->name + " has value type " + std::to_string(t->type) + "; expected F32";
+    }
+    return {};
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_options* opts, ribn_rocm_model** out,
+                                   char* err, size_t err_len) {
+    if (!path || !out) { set_err(err, err_len, "null argument"); return RIBN_ERR_INVALID; }
+    *out = nullptr;
+    GgufFile g;
+    std::string msg = g.open(path);
+    if (!msg.empty()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+    std::string arch;
+    if (!g.get_str("general.architecture", &arch)) { set_err(err, err_len, "missing general.architecture"); return RIBN_ERR_FORMAT; }
+    if (arch != "qwen2" && arch != "qwen3") {
+        set_err(err, err_len, "general.architecture `" + arch + "` is not supported (expected qwen2 or qwen3)");
+        return RIBN_ERR_FORMAT;
+    }
+    std::unique_ptr<ribn_rocm_model, void (*)(ribn_rocm_model*)> Mp(new ribn_rocm_model(), ribn_rocm_free);
+    ribn_rocm_model* M = Mp.get();
+    M->qwen3 = arch == "qwen3";
+    auto need_u = [&](const char* suffix, int* dst) -> bool {
+        uint64_t v;
+        if (!g.get_u64(arch + "." + suffix, &v) || v == 0 || v > (1u << 30)) {
+            set_err(err, err_len, "missing or invalid " + arch + "." + suffix);
+            return false;
+        }
+        *dst = (int)v;
+        return true;
+    };
+    if (!need_u("embedding_length", &M->H) || !need_u("block_count", &M->L) || !need_u("attention.head_count", &M->hq) ||
+        !need_u("attention.head_count_kv", &M->hkv) || !need_u("feed_forward_length", &M->F))
+        return RIBN_ERR_FORMAT;
+    uint64_t v;
+    M->hd = g.get_u64(arch + ".attention.key_length", &v) ? (int)v : M->H / M->hq;
+    M->rot = g.get_u64(arch + ".rope.dimension_count", &v) ? (int)v : M->hd;
+    if (!g.get_f32(arch + ".attention.layer_norm_rms_epsilon", &M->eps)) M->eps = 1e-6f;
+    if (!g.get_f32(arch + ".rope.freq_base", &M->base)) M->base = 10000.f;
+    uint64_t vlen;
+    if (g.get_u64(arch + ".attention.value_length", &vlen) && (int)vlen != M->hd) {
+        set_err(err, err_len, arch + ".attention.value_length must equal key_length"); return RIBN_ERR_FORMAT;
+    }
+    if ((M->hd != 64 && M->hd != 128) || M->rot > M->hd || M->rot % 2) {
+        set_err(err, err_len, arch + ".attention.key_length " + std::to_string(M->hd) + " is not supported (64 or 128)");
+        return RIBN_ERR_FORMAT;
+    }
+    if (M->hq % M->hkv || M->hq / M->hkv > 8) {
+        set_err(err, err_len, arch + ".attention.head_count / head_count_kv must be an integer <= 8");
+        return RIBN_ERR_FORMAT;
+    }
+    if (M->H % 256 || M->F % 256 || M->H > 16384 || M->F > 28672) {
+        set_err(err, err_len, arch + ".embedding_length and feed_forward_length must be multiples of 256 "
+                                     "(<= 16384 / 28672)");
+        return RIBN_ERR_FORMAT;
+    }
+    const GgufTensor* te = g.tensor("token_embd.weight");
+    if ((msg = validate_type(te, "token_embd.weight", true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+    if (te->dims.size() != 2 || (int)te->dims[0] != M->H) {
+        set_err(err, err_len, "token_embd.weight must be [embedding_length, vocab]"); return RIBN_ERR_FORMAT;
+    }
+    M->V = (int)te->dims[1];
+    const GgufTensor* to = g.tensor("output.weight");
+    if (!to) to = te;   // tied head
+    if ((msg = validate_type(to, "output.weight", true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+    const GgufTensor* ton = g.tensor("output_norm.weight");
+    if ((msg = validate_type(ton, "output_norm.weight", false)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+
+    uint64_t ctx_meta = 0;
+    g.get_u64(arch + ".context_length", &ctx_meta);
+    ribn_rocm_load_options o{};
+    if (opts) o = *opts;
+    M->context = o.context_tokens ? o.context_tokens : (uint32_t)std::min<uint64_t>(ctx_meta ? ctx_meta : 4096, 4096);
+    M->max_seqs = o.max_sequences ? o.max_sequences : 8;
+    M->max_batch_tokens = o.max_batch_tokens ? o.max_batch_tokens : 2048;
+    M->max_pages = (int)((M->context + kPageTokens - 1) / kPageTokens);
+    M->kv_pages = o.kv_pages ? o.kv_pages : (uint32_t)(M->max_seqs * M->max_pages);
+    if ((int)M->kv_pages < M->max_pages) M->kv_pages = M->max_pages;
+    M->device = o.device;
+    M->name = "ribn-rocm " + arch + " " + std::to_string(M->L) + "x" + std::to_string(M->H);
+
+    HIPCHK(hipSetDevice(M->device));
+    HIPCHK(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking));
+    std::vector<uint8_t> staging;
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    auto upload_mat = [&](const GgufTensor* t, uint64_t rows, uint64_t k, QMat* q) -> int {
+        if (t->dims.size() != 2 || t->dims[0] != k || t->dims[1] != rows) {
+            return fail(nullptr, err, err_len,
+                        "tensor " + t->name + " has shape [" + std::to_string(t->dims[0]) + ", " +
+                            std::to_string(t->dims.size() > 1 ? t->dims[1] : 0) + "], expected [" + std::to_string(k) +
+                            ", " + std::to_string(rows) + "]",
+                        RIBN_ERR_FORMAT);
+        }
+        HIPCHK(upload_qmat(M, t->type, rows, k, g.data(*t), q, staging));
+        return RIBN_OK;
+    };
+    auto upload_f32 = [&](const GgufTensor* t, uint64_t n, float** dst) -> int {
+        if (t->type != GGML_F32 || t->dims.empty() || t->dims[0] != n)
+            return fail(nullptr, err, err_len, "tensor " + t->name + " must be F32 [" + std::to_string(n) + "]", RIBN_ERR_FORMAT);
+        HIPCHK(dalloc(M, dst, n * 4));
+        HIPCHK(hipMemcpy(*dst, g.data(*t), n * 4, hipMemcpyHostToDevice));
+        return RIBN_OK;
+    };
+    int rc;
+    if ((rc = upload_mat(te, M->V, M->H, &M->embd)) != RIBN_OK) return rc;
+    if (to == te) M->out = M->embd;
+    else if ((rc = upload_mat(to, M->V, M->H, &M->out)) != RIBN_OK) return rc;
+    if ((rc = upload_f32(ton, M->H, &M->out_norm)) != RIBN_OK) return rc;
+    M->layers.resize(M->L);
+    for (int l = 0; l < M->L; l++) {
+        Layer& y = M->layers[l];
+        auto T = [&](const char* nm) { return g.tensor("blk." + std::to_string(l) + "." + nm); };
+        struct { const char* n; uint64_t rows, k; QMat* q; } mats[] = {
+            {"attn_q.weight", (uint64_t)qd, (uint64_t)M->H, &y.q},     {"attn_k.weight", (uint64_t)kd, (uint64_t)M->H, &y.k},
+            {"attn_v.weight", (uint64_t)kd, (uint64_t)M->H, &y.v},     {"attn_output.weight", (uint64_t)M->H, (uint64_t)qd, &y.o},
+            {"ffn_gate.weight", (uint64_t)M->F, (uint64_t)M->H, &y.gate}, {"ffn_up.weight", (uint64_t)M->F, (uint64_t)M->H, &y.up},
+            {"ffn_down.weight", (uint64_t)M->H, (uint64_t)M->F, &y.down},
+        };
+        for (auto& m : mats) {
+            const GgufTensor* t = T(m.n);
+            std::string nm = "blk." + std::to_string(l) + "." + m.n;
+            if ((msg = validate_type(t, nm.c_str(), true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+            if ((rc = upload_mat(t, m.rows, m.k, m.q)) != RIBN_OK) return rc;
+        }
+        if (y.gate.type != y.up.type) {
+            set_err(err, err_len, "ffn_gate and ffn_up must share a value type"); return RIBN_ERR_FORMAT;
+        }
+        struct { const char* n; uint64_t len; float** dst; bool req; } vecs[] = {
+            {"attn_norm.weight", (uint64_t)M->H, &y.attn_norm, true}, {"ffn_norm.weight", (uint64_t)M->H, &y.ffn_norm, true},
+            {"attn_q_norm.weight", (uint64_t)M->hd, &y.q_norm, false}, {"attn_k_norm.weight", (uint64_t)M->hd, &y.k_norm, false},
+            {"attn_q.bias", (uint64_t)qd, &y.q_bias, false},          {"attn_k.bias", (uint64_t)kd, &y.k_bias, false},
+            {"attn_v.bias", (uint64_t)kd, &y.v_bias, false},
+        };
+        for (auto& vv : vecs) {
+            const GgufTensor* t = T(vv.n);
+            if (!t) {
+                if (vv.req) { set_err(err, err_len, "missing tensor blk." + std::to_string(l) + "." + vv.n); return RIBN_ERR_FORMAT; }
+                continue;
+            }
+            if ((rc = upload_f32(t, vv.len, vv.dst)) != RIBN_OK) return rc;
+        }
+        const size_t kv_layer = (size_t)M->kv_pages * M->hkv * kPageTokens * M->hd;
+        HIPCHK(dalloc(M, &y.kc, kv_layer * 2));
+        HIPCHK(dalloc(M, &y.vc, kv_layer * 2));
+        HIPCHK(hipMemsetAsync(y.kc, 0, kv_layer * 2, M->stream));
+        HIPCHK(hipMemsetAsync(y.vc, 0, kv_layer * 2, M->stream));
+        M->kv_bytes += kv_layer * 4;
+    }
+    staging.clear();
+    staging.shrink_to_fit();
+
+    HIPCHK(dalloc(M, &M->h, sizeof(float) * M->H));
+    HIPCHK(dalloc(M, &M->raw, sizeof(float) * (qd + 2 * kd)));
+    HIPCHK(dalloc(M, &M->qbuf, sizeof(float) * qd));
+    HIPCHK(dalloc(M, &M->attn, sizeof(float) * qd));
+    HIPCHK(dalloc(M, &M->act, sizeof(float) * M->F));
+    HIPCHK(dalloc(M, &M->logits, sizeof(float) * M->V));
+    HIPCHK(dalloc(M, &M->part, sizeof(float) * (size_t)qd / M->hd * kMaxSplits * (M->hd + 2)));
+    const int n_counters = M->hq + 2 * M->hkv + 1;
+    HIPCHK(dalloc(M, &M->counters, sizeof(uint32_t) * n_counters));
+    HIPCHK(hipMemsetAsync(M->counters, 0, sizeof(uint32_t) * n_counters, M->stream));
+    HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * ((size_t)M->V / 2 + 64)));
+
+    const int slots = (int)M->max_seqs + 1;
+    HIPCHK(dalloc(M, &M->d_slots, sizeof(SeqState) * slots));
+    HIPCHK(dalloc(M, &M->d_pages, sizeof(int32_t) * (size_t)slots * M->max_pages));
+    HIPCHK(dalloc(M, &M->d_tokens, sizeof(uint32_t) * (size_t)slots * (M->context + 1)));
+    HIPCHK(dalloc(M, &M->d_ctl, sizeof(StepCtl)));
+    HIPCHK(halloc(M, &M->h_slot_ptr, sizeof(SeqState*) * slots));
+    HIPCHK(halloc(M, &M->h_state, sizeof(SeqState) * slots));
+    HIPCHK(halloc(M, &M->h_pages, sizeof(int32_t) * (size_t)slots * M->max_pages));
+    HIPCHK(halloc(M, &M->h_tokens, sizeof(uint32_t) * (size_t)slots * (M->context + 1)));
+    HIPCHK(halloc(M, &M->h_out, sizeof(uint32_t) * (M->max_seqs + 8)));
+    for (int s = 0; s < slots; s++) {
+        M->h_slot_ptr[s] = &M->d_slots[s];
+        SeqState& st = M->h_state[s];
+        st.pos = 0;
+        st.last_token = 0;
+        st.max_pages = M->max_pages;
+        st.max_ctx = (int)M->context;
+        st.pages = M->d_pages + (size_t)s * M->max_pages;
+        st.tokens = M->d_tokens + (size_t)s * (M->context + 1);
+    }
+    HIPCHK(hipMemcpyAsync(M->d_slots, M->h_state, sizeof(SeqState) * slots, hipMemcpyHostToDevice, M->stream));
+    HIPCHK(hipMemcpyAsync(M->d_ctl, &M->h_slot_ptr[slots - 1], sizeof(SeqState*), hipMemcpyHostToDevice, M->stream));
+    HIPCHK(hipStreamSynchronize(M->stream));
+    for (int s = (int)M->max_seqs - 1; s >= 0; s--) M->free_slots.push_back(s);
+    for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
+    build_launches(M);
+    *out = Mp.release();
+    return RIBN_OK;
+}
+
+extern "C" void ribn_rocm_free(ribn_rocm_model* M) {
+    if (!M) return;
+    if (M->stream) hipStreamSynchronize(M->stream);
+    for (auto& kv : M->graphs) hipGraphExecDestroy(kv.second);
+    if (M->pending.done) hipEventDestroy(M->pending.done);
+    for (void* p : M->dev_allocs) hipFree(p);
+    for (void* p : M->host_allocs) hipHostFree(p);
+    if (M->stream) hipStreamDestroy(M->stream);
+    delete M;
+}
+
+extern "C" int ribn_rocm_info(const ribn_rocm_model* M, ribn_rocm_info_t* o) {
+    if (!M || !o) return RIBN_ERR_INVALID;
+    std::memset(o, 0, sizeof(*o));
+    std::snprintf(o->name, sizeof(o->name), "%s", M->name.c_str());
+    o->context_tokens = M->context;
+    o->max_sequences = M->max_seqs;
+    o->max_batch_tokens = M->max_batch_tokens;
+    o->max_decode_tokens = 1;
+    o->hidden = M->H; o->layers = M->L; o->q_heads = M->hq; o->kv_heads = M->hkv;
+    o->head_dim = M->hd; o->ffn = M->F; o->vocab = M->V; o->rope_dims = M->rot;
+    o->weight_bytes = M->weight_bytes;
+    o->kv_bytes = M->kv_bytes;
+    return RIBN_OK;
+}
+
+// ---------------------------------------------------------------------------
+extern "C" int ribn_rocm_generate(ribn_rocm_model* M, const uint32_t* prompt, uint32_t n_prompt, uint32_t n_new,
+                                  uint32_t* out_tokens, ribn_rocm_timing* timing, char* err, size_t err_len) {
+    if (!M || !prompt || !out_tokens) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
+    if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    if (n_prompt == 0 || n_new == 0 || (uint64_t)n_prompt + n_new > M->context)
+        return fail(nullptr, err, err_len, "prompt/output length outside the prepared context", RIBN_ERR_INVALID);
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
+    std::vector<int32_t> pages;
+    if (!take_pages(M, n_prompt + n_new, &pages))
+        return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
+    const int slot = (int)M->max_seqs;
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    auto cleanup = [&]() {
+        if (e0) hipEventDestroy(e0);
+        if (e1) hipEventDestroy(e1);
+        if (e2) hipEventDestroy(e2);
+        give_pages(M, pages);
+    };
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventCreate(&e2);
+    if (e == hipSuccess) e = reset_slot(M, slot, pages, prompt, n_prompt);
+    if (e == hipSuccess) e = select_slot(M, slot);
+    if (e == hipSuccess) e = hipEventRecord(e0, M->stream);
+    for (uint32_t p = 0; e == hipSuccess && p + 1 < n_prompt; p++) e = graph_step(M, false, (int)p + 1);
+    if (e == hipSuccess) e = graph_step(M, true, (int)n_prompt);
+    if (e == hipSuccess) e = hipEventRecord(e1, M->stream);
+    for (uint32_t t = 1; e == hipSuccess && t < n_new; t++) e = graph_step(M, true, (int)(n_prompt + t));
+    if (e == hipSuccess) e = hipEventRecord(e2, M->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(out_tokens, M->d_tokens + (size_t)slot * (M->context + 1) + n_prompt, sizeof(uint32_t) * n_new,
+                           hipMemcpyDeviceToHost, M->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(M->stream);
+    if (e == hipSuccess && timing) {
+        float a = 0.f, b = 0.f;
+        hipEventElapsedTime(&a, e0, e1);
+        hipEventElapsedTime(&b, e1, e2);
+        timing->prefill_ms = a;
+        timing->decode_ms = b;
+        timing->prefill_tokens = n_prompt;
+        timing->decode_tokens = n_new - 1;
+    }
+    cleanup();
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("generate", e));
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_trace(ribn_rocm_model* M, const uint32_t* tokens, uint32_t n, uint32_t* argmax_out,
+                               float* logits_out, float* hidden_out, char* err, size_t err_len) {
+    if (!M || !tokens || !argmax_out) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
+    if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    if (n == 0 || n + 1 > M->context) return fail(nullptr, err, err_len, "trace length outside the context", RIBN_ERR_INVALID);
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
+    std::vector<int32_t> pages;
+    if (!take_pages(M, n + 1, &pages)) return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
+    const int slot = (int)M->max_seqs;
+    float* dtrace = nullptr;
+    hipError_t e = hipSuccess;
+    if (hidden_out) e = hipMalloc(&dtrace, sizeof(float) * (size_t)(M->L + 1) * M->H);
+    if (e == hipSuccess) e = reset_slot(M, slot, pages, tokens, n);
+    if (e == hipSuccess) e = select_slot(M, slot);
+    uint32_t* dtok = M->d_tokens + (size_t)slot * (M->context + 1);
+    for (uint32_t p = 0; e == hipSuccess && p < n; p++) {
+        e = enqueue_step(M, true, splits_for_ctx((int)p + 1), dtrace);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(&M->h_out[0], &M->d_slots[slot].last_token, 4, hipMemcpyDeviceToHost, M->stream);
+        if (e == hipSuccess && logits_out)
+            e = hipMemcpyAsync(logits_out + (size_t)p * M->V, M->logits, sizeof(float) * M->V, hipMemcpyDeviceToHost, M->stream);
+        if (e == hipSuccess && hidden_out)
+            e = hipMemcpyAsync(hidden_out + (size_t)p * (M->L + 1) * M->H, dtrace, sizeof(float) * (M->L + 1) * M->H,
+                               hipMemcpyDeviceToHost, M->stream);
+        // teacher forcing: restore the given next token over the sampled one
+        if (e == hipSuccess && p + 1 < n)
+            e = hipMemcpyAsync(dtok + p + 1, M->h_tokens + (size_t)slot * (M->context + 1) + p + 1, 4,
+                               hipMemcpyHostToDevice, M->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(M->stream);
+        if (e == hipSuccess) argmax_out[p] = M->h_out[0];
+    }
+    if (dtrace) hipFree(dtrace);
+    give_pages(M, pages);
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("trace", e));
+    return RIBN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// GenerationExecutor (executor.rs:171-254) with the Qwen adapter's rules
+// (crates/qwen/src/execution.rs:80-414).
+extern "C" int ribn_rocm_admit(ribn_rocm_model* M, uint64_t request_id, uint64_t sequence, const uint32_t* tokens,
+                               uint32_t n_tokens, const ribn_rocm_token_options* opt, int32_t* admission, char* err,
+                               size_t err_len) {
+    (void)request_id;
+    if (!M || !admission || !opt) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
+    if (M->seqs.count(sequence)) return fail(nullptr, err, err_len, "duplicate sequence", RIBN_ERR_INVALID);
+    const uint64_t total = (uint64_t)n_tokens + opt->max_output_tokens;
+    bool bad = n_tokens == 0 || !tokens || opt->max_output_tokens == 0 || total > M->context;
+    for (uint32_t i = 0; !bad && i < n_tokens; i++) bad = tokens[i] >= (uint32_t)M->V;
+    for (uint32_t i = 0; !bad && i < opt->n_stop_tokens; i++) bad = opt->stop_tokens[i] >= (uint32_t)M->V;
+    if (bad) {
+        *admission = RIBN_ADMIT_REJECTED;
+        set_err(err, err_len, "Qwen input/output limits or token IDs are invalid");
+        return RIBN_OK;
+    }
+    if (opt->temperature != 0.0f) {
+        *admission = RIBN_ADMIT_REJECTED;
+        set_err(err, err_len, "the ROCm Qwen executor currently supports greedy sampling only");
+        return RIBN_OK;
+    }
+    const uint64_t need = (total + kPageTokens - 1) / kPageTokens;
+    if (need > M->kv_pages) {
+        *admission = RIBN_ADMIT_REJECTED;
+        set_err(err, err_len, "Qwen needs " + std::to_string(need) + " KV pages, above the " +
+                                  std::to_string(M->kv_pages) + "-page pool");
+        return RIBN_OK;
+    }
+    if (M->free_slots.empty() || M->free_pages.size() < need) {
+        *admission = RIBN_ADMIT_DEFERRED;
+        set_err(err, err_len, "waiting for sequence capacity");
+        return RIBN_OK;
+    }
+    Sequence s;
+    s.slot = M->free_slots.back();
+    take_pages(M, (uint32_t)total, &s.pages);
+    s.prompt_len = n_tokens;
+    hipError_t e = reset_slot(M, s.slot, s.pages, tokens, n_tokens);
+    if (e != hipSuccess) {
+        give_pages(M, s.pages);
+        return fail(M, err, err_len, hip_msg("admit", e));
+    }
+    M->free_slots.pop_back();
+    M->seqs.emplace(sequence, std::move(s));
+    *admission = RIBN_ADMIT_READY;
+    if (err && err_len) err[0] = 0;
+    return RIBN_OK;
+}
+
+namespace {
+int check_item(ribn_rocm_model* M, const ribn_rocm_batch_item& it, char* err, size_t err_len) {
+    auto s = M->seqs.find(it.sequence);
+    if (s == M->seqs.end()) return fail(nullptr, err, err_len, "unknown Qwen sequence", RIBN_ERR_INVALID);
+    if (s->second.in_flight) return fail(nullptr, err, err_len, "Qwen sequence is in flight", RIBN_ERR_INVALID);
+    const uint64_t end = (uint64_t)it.prefix + it.token_budget;
+    if (it.token_budget == 0 || s->second.committed != it.prefix || end > M->context)
+        return fail(nullptr, err, err_len, "Qwen work does not match the sequence prefix/capacity", RIBN_ERR_INVALID);
+    if (it.kind == RIBN_STEP_PREFILL) {
+        if (end > s->second.prompt_len || it.output_budget != (end == s->second.prompt_len ? 1u : 0u))
+            return fail(nullptr, err, err_len, "Qwen prefill boundary/output mismatch", RIBN_ERR_INVALID);
+    } else if (it.kind == RIBN_STEP_DECODE) {
+        if (it.token_budget != 1 || it.output_budget != 1 || it.prefix < s->second.prompt_len)
+            return fail(nullptr, err, err_len, "Qwen adapter only supports one-token ordinary decode", RIBN_ERR_INVALID);
+        if (!s->second.has_next) return fail(nullptr, err, err_len, "Qwen decode has no next token", RIBN_ERR_INVALID);
+    } else {
+        return fail(nullptr, err, err_len, "unknown step kind", RIBN_ERR_INVALID);
+    }
+    return RIBN_OK;
+}
+bool same_items(const std::vector<ribn_rocm_batch_item>& a, const ribn_rocm_batch_item* b, size_t n) {
+    if (a.size() != n) return false;
+    for (size_t i = 0; i < n; i++)
+        if (a[i].sequence != b[i].sequence || a[i].kind != b[i].kind || a[i].prefix != b[i].prefix ||
+            a[i].token_budget != b[i].token_budget || a[i].output_budget != b[i].output_budget)
+            return false;
+    return true;
+}
+}  // namespace
+
+extern "C" int ribn_rocm_prepare(ribn_rocm_model* M, const ribn_rocm_batch_item* items, size_t n, char* err,
+                                 size_t err_len) {
+    if (!M || (!items && n)) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted || M->has_pending || M->has_prepared)
+        return fail(nullptr, err, err_len, "Qwen execution is faulted or busy", M->faulted ? RIBN_ERR_FAULTED : RIBN_ERR_BUSY);
+    uint64_t tokens = 0;
+    for (size_t i = 0; i < n; i++) tokens += items[i].token_budget;
+    if (n > M->max_seqs || tokens > M->max_batch_tokens)
+        return fail(nullptr, err, err_len, "Qwen batch exceeds prepared limits", RIBN_ERR_CAPACITY);
+    for (size_t i = 0; i < n; i++) {
+        int rc = check_item(M, items[i], err, err_len);
+        if (rc) return rc;
+        for (size_t j = 0; j < i; j++)
+            if (items[j].sequence == items[i].sequence)
+                return fail(nullptr, err, err_len, "duplicate sequence in batch", RIBN_ERR_INVALID);
+    }
+    M->prepared.assign(items, items + n);
+    M->has_prepared = true;
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_abandon(ribn_rocm_model* M, char* err, size_t err_len) {
+    if (!M) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    M->has_prepared = false;
+    M->prepared.clear();
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* items, size_t n, uint64_t* submission,
+                                char* err, size_t err_len) {
+    if (!M || !submission || (!items && n)) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted || M->has_pending)
+        return fail(nullptr, err, err_len, "Qwen execution is faulted or busy", M->faulted ? RIBN_ERR_FAULTED : RIBN_ERR_BUSY);
+    if (!M->has_prepared) return fail(nullptr, err, err_len, "Qwen batch was not prepared", RIBN_ERR_INVALID);
+    if (!same_items(M->prepared, items, n))
+        return fail(nullptr, err, err_len, "Qwen submission differs from its preparation", RIBN_ERR_INVALID);
+    M->has_prepared = false;
+    M->prepared.clear();
+    hipError_t e = hipSuccess;
+    if (!M->pending.done) e = hipEventCreateWithFlags(&M->pending.done, hipEventDisableTiming);
+    for (size_t r = 0; e == hipSuccess && r < n; r++) {
+        const ribn_rocm_batch_item& it = items[r];
+        Sequence& s = M->seqs[it.sequence];
+        s.in_flight = true;
+        e = select_slot(M, s.slot);
+        const uint32_t end = it.prefix + it.token_budget;
+        for (uint32_t p = it.prefix; e == hipSuccess && p < end; p++) {
+            const bool head = (p + 1 == end) && it.output_budget > 0;
+            e = graph_step(M, head, (int)p + 1);
+        }
+        if (e == hipSuccess && it.output_budget > 0)
+            e = hipMemcpyAsync(&M->h_out[r], &M->d_slots[s.slot].last_token, 4, hipMemcpyDeviceToHost, M->stream);
+    }
+    if (e == hipSuccess) e = hipEventRecord(M->pending.done, M->stream);
+    M->pending.items.assign(items, items + n);
+    M->pending.id = M->next_submission++;
+    M->has_pending = true;
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("submit", e));
+    *submission = M->pending.id;
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_poll(ribn_rocm_model* M, uint64_t submission, ribn_rocm_step_completion* out, size_t cap,
+                              size_t* n_out, char* err, size_t err_len) {
+    if (!M || !n_out) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (!M->has_pending) return fail(nullptr, err, err_len, "unknown Qwen submission", RIBN_ERR_INVALID);
+    if (M->pending.id != submission) return fail(nullptr, err, err_len, "Qwen submission identity mismatch", RIBN_ERR_INVALID);
+    if (cap < M->pending.items.size()) return fail(nullptr, err, err_len, "completion array too small", RIBN_ERR_INVALID);
+    hipError_t e = hipEventQuery(M->pending.done);
+    if (e == hipErrorNotReady) return RIBN_PENDING;
+    const std::vector<ribn_rocm_batch_item> items = M->pending.items;
+    M->has_pending = false;
+    for (auto& it : items) M->seqs[it.sequence].in_flight = false;
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("poll", e));
+    for (size_t r = 0; r < items.size(); r++) {
+        const auto& it = items[r];
+        Sequence& s = M->seqs[it.sequence];
+        const uint32_t prefix = it.prefix + it.token_budget;
+        ribn_rocm_step_completion c{};
+        c.sequence = it.sequence;
+        c.prefix = prefix;
+        if (it.output_budget > 0) {
+            const uint32_t tok = M->h_out[r];
+            if (tok >= (uint32_t)M->V) return fail(M, err, err_len, "Qwen completion does not match submitted work");
+            c.n_tokens = 1;
+            c.token = tok;
+            s.next = tok;
+            s.has_next = true;
+        }
+        s.committed = prefix;
+        out[r] = c;
+    }
+    *n_out = items.size();
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_release(ribn_rocm_model* M, uint64_t sequence, char* err, size_t err_len) {
+    if (!M) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    auto it = M->seqs.find(sequence);
+    if (it == M->seqs.end()) return RIBN_OK;
+    if (it->second.in_flight) return fail(nullptr, err, err_len, "Qwen sequence is in flight", RIBN_ERR_BUSY);
+    give_pages(M, it->second.pages);
+    M->free_slots.push_back(it->second.slot);
+    M->seqs.erase(it);
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_synchronize(ribn_rocm_model* M, char* err, size_t err_len) {
+    if (!M) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    M->has_prepared = false;
+    M->prepared.clear();
+    hipError_t e = hipStreamSynchronize(M->stream);
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("synchronize", e));
+    return RIBN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel-level entry points.
+namespace {
+struct Scoped {
+    std::vector<void*> p;
+    ~Scoped() { for (void* x : p) hipFree(x); }
+    template <typename T>
+    hipError_t alloc(T** out, size_t bytes) {
+        void* v = nullptr;
+        hipError_t e = hipMalloc(&v, bytes ? bytes : 256);
+        if (e == hipSuccess) { p.push_back(v); *out = static_cast<T*>(v); }
+        return e;
+    }
+};
+
+hipError_t upload_plain(Scoped& S, uint32_t type, uint64_t rows, uint64_t k, const uint8_t* blocks, QMat* q) {
+    uint64_t be, bb;
+    type_layout(type, &be, &bb);
+    const uint64_t nblocks = rows * (k / be);
+    size_t sa, sb, sc, sd;
+    plane_sizes(type, nblocks, &sa, &sb, &sc, &sd);
+    const size_t total = align256(sa) + align256(sb) + align256(sc) + align256(sd);
+    std::vector<uint8_t> host(total);
+    uint8_t* ha = host.data();
+    uint8_t *hb = ha + align256(sa), *hc = hb + align256(sb), *hd = hc + align256(sc);
+    if (blocks) retile(type, blocks, nblocks, ha, hb, hc, hd);
+    else {
+        // benchmark fill: random quants with finite unit-range scales
+        uint64_t x = 0x9e3779b97f4a7c15ull;
+        for (size_t i = 0; i < total; i++) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; host[i] = (uint8_t)x; }
+        auto put_half = [](uint8_t* p, uint16_t h) { p[0] = (uint8_t)h; p[1] = (uint8_t)(h >> 8); };
+        for (uint64_t i = 0; i < nblocks; i++) {
+            if (type == GGML_Q4_K) { put_half(hb + i * 16, 0x2000); put_half(hb + i * 16 + 2, 0x2000); }
+            else if (type == GGML_Q6_K) put_half(hd + i * 2, 0x2000);
+            else put_half(hb + i * 2, 0x2000);
+        }
+    }
+    uint8_t* dev = nullptr;
+    hipError_t e = S.alloc(&dev, total);
+    if (e != hipSuccess) return e;
+    if ((e = hipMemcpy(dev, host.data(), total, hipMemcpyHostToDevice)) != hipSuccess) return e;
+    QMat m{};
+    m.type = type; m.rows = (uint32_t)rows; m.k = (uint32_t)k; m.nb = (uint32_t)(k / be);
+    m.a = dev; m.b = dev + (hb - ha); m.c = dev + (hc - ha); m.d = dev + (hd - ha);
+    *q = m;
+    return hipSuccess;
+}
+
+std::string check_shape(uint32_t type, uint64_t rows, uint64_t k) {
+    if (type != GGML_Q4_K && type != GGML_Q6_K && type != GGML_Q8_0) return "unsupported value type " + std::to_string(type);
+    uint64_t be, bb;
+    type_layout(type, &be, &bb);
+    if (rows == 0 || k == 0 || k % be || k % 16) return "k must be a positive multiple of the block size";
+    if (rows > (1u << 30) || k > 28672) return "matrix too large for the matvec kernel (k <= 28672)";
+    return {};
+}
+}  // namespace
+
+extern "C" int ribn_rocm_dequantize(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t k, float* out,
+                                    char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string m = check_shape(type, rows, k);
+    if (!m.empty() || !blocks || !out) return fail(nullptr, err, err_len, m.empty() ? "null argument" : m, RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    float* dout = nullptr;
+    HIPCHK(upload_plain(S, type, rows, k, blocks, &q));
+    HIPCHK(S.alloc(&dout, sizeof(float) * rows * k));
+    HIPCHK(launch_dequant(q, dout, nullptr));
+    HIPCHK(hipMemcpy(out, dout, sizeof(float) * rows * k, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_gemv(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t k, const float* x,
+                              const float* rms_weight, float eps, float* y, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string m = check_shape(type, rows, k);
+    if (!m.empty() || !blocks || !x || !y) return fail(nullptr, err, err_len, m.empty() ? "null argument" : m, RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    float *dx = nullptr, *dw = nullptr, *dy = nullptr;
+    HIPCHK(upload_plain(S, type, rows, k, blocks, &q));
+    HIPCHK(S.alloc(&dx, sizeof(float) * k));
+    HIPCHK(S.alloc(&dy, sizeof(float) * rows));
+    HIPCHK(hipMemcpy(dx, x, sizeof(float) * k, hipMemcpyHostToDevice));
+    if (rms_weight) {
+        HIPCHK(S.alloc(&dw, sizeof(float) * k));
+        HIPCHK(hipMemcpy(dw, rms_weight, sizeof(float) * k, hipMemcpyHostToDevice));
+    }
+    MvArgs a = mv_base(dx, dw, eps, (int)k, MV_STORE, nullptr);
+    a.nseg = 1;
+    a.seg[0].w = q;
+    a.seg[0].out = dy;
+    a.items_per_wave = choose_ipw((int)(rows / 2), 4);
+    const int nwg = layout_segments(a);
+    HIPCHK(launch_matvec(a, nwg, nullptr));
+    HIPCHK(hipMemcpy(y, dy, sizeof(float) * rows, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, uint32_t iters, double* avg_ms, char* err,
+                                    size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string m = check_shape(type, rows, k);
+    if (!m.empty() || !avg_ms || iters == 0) return fail(nullptr, err, err_len, m.empty() ? "bad argument" : m, RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    float *dx = nullptr, *dy = nullptr;
+    HIPCHK(upload_plain(S, type, rows, k, nullptr, &q));
+    HIPCHK(S.alloc(&dx, sizeof(float) * k));
+    HIPCHK(S.alloc(&dy, sizeof(float) * rows));
+    std::vector<float> hx(k, 0.5f);
+    HIPCHK(hipMemcpy(dx, hx.data(), sizeof(float) * k, hipMemcpyHostToDevice));
+    MvArgs a = mv_base(dx, nullptr, 0.f, (int)k, MV_STORE, nullptr);
+    a.nseg = 1;
+    a.seg[0].w = q;
+    a.seg[0].out = dy;
+    a.items_per_wave = choose_ipw((int)(rows / 2), 4);
+    const int nwg = layout_segments(a);
+    hipStream_t st;
+    HIPCHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    for (int i = 0; i < 3; i++) HIPCHK(launch_matvec(a, nwg, st));
+    HIPCHK(hipEventRecord(e0, st));
+    for (uint32_t i = 0; i < iters; i++) HIPCHK(launch_matvec(a, nwg, st));
+    HIPCHK(hipEventRecord(e1, st));
+    HIPCHK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+    *avg_ms = ms / iters;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipStreamDestroy(st);
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, uint32_t iters, double* avg_ms,
+                                            uint64_t* bytes, char* err, size_t err_len) {
+    if (!M || !avg_ms || !bytes || iters == 0) return fail(nullptr, err, err_len, "bad argument", RIBN_ERR_INVALID);
+    if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
+    MvArgs a;
+    int nwg;
+    auto qbytes = [](const QMat& q) {
+        uint64_t be, bb;
+        type_layout(q.type, &be, &bb);
+        return (uint64_t)q.rows * q.nb * bb;
+    };
+    switch (which) {
+    case 0: a = M->mv_gu[0]; nwg = M->wg_gu[0]; *bytes = qbytes(a.seg[0].w) + qbytes(a.seg[0].w2); break;
+    case 1: a = M->mv_down[0]; nwg = M->wg_down[0]; a.mode = MV_STORE; a.seg[0].out = M->act; *bytes = qbytes(a.seg[0].w); break;
+    case 2: a = M->mv_head; nwg = M->head_wgs; a.mode = MV_STORE; *bytes = qbytes(a.seg[0].w); break;
+    default: return fail(nullptr, err, err_len, "unknown kernel selector", RIBN_ERR_INVALID);
+    }
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    for (int i = 0; i < 3; i++) HIPCHK(launch_matvec(a, nwg, M->stream));
+    HIPCHK(hipEventRecord(e0, M->stream));
+    for (uint32_t i = 0; i < iters; i++) HIPCHK(launch_matvec(a, nwg, M->stream));
+    HIPCHK(hipEventRecord(e1, M->stream));
+    HIPCHK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+    *avg_ms = ms / iters;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_argmax(const float* logits, uint64_t n, uint32_t* out, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    if (!logits || !out || n == 0 || n > 0xffffffffull) return fail(nullptr, err, err_len, "bad argument", RIBN_ERR_INVALID);
+    Scoped S;
+    float* dl = nullptr;
+    uint64_t* part = nullptr;
+    uint32_t *ctr = nullptr, *dout = nullptr;
+    HIPCHK(S.alloc(&dl, sizeof(float) * n));
+    HIPCHK(S.alloc(&part, sizeof(uint64_t) * 1024));
+    HIPCHK(S.alloc(&ctr, sizeof(uint32_t) * 2));
+    dout = ctr + 1;
+    HIPCHK(hipMemset(ctr, 0, 8));
+    HIPCHK(hipMemcpy(dl, logits, sizeof(float) * n, hipMemcpyHostToDevice));
+    HIPCHK(launch_argmax(dl, (uint32_t)n, part, ctr, dout, nullptr));
+    HIPCHK(hipMemcpy(out, dout, 4, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
