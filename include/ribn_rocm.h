@@ -56,8 +56,11 @@ typedef struct {
     uint32_t max_batch_tokens; /* 0 -> 2048 */
     uint32_t kv_pages;         /* 16-token BF16 pages in the pool (0 -> max_sequences*context/16) */
     int32_t device;            /* HIP device ordinal */
-    uint32_t flags;            /* reserved, 0 */
+    uint32_t flags;            /* RIBN_LOAD_* bits */
 } ribn_rocm_load_options;
+/* KV cache in binary16 (the reference CUDA cache type, nvidia/src/model_ops.rs:1258)
+ * instead of the default bfloat16. */
+#define RIBN_LOAD_KV_F16 1u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);
@@ -74,7 +77,8 @@ typedef struct {
     /* model geometry */
     uint32_t hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, rope_dims;
     uint64_t weight_bytes;     /* encoded bytes of all matrices on device */
-    uint64_t kv_bytes;         /* BF16 KV pool bytes */
+    uint64_t kv_bytes;         /* KV pool bytes */
+    uint32_t kv_f16;           /* 1: binary16 KV cache, 0: bfloat16 */
 } ribn_rocm_info_t;
 int ribn_rocm_info(const ribn_rocm_model *model, ribn_rocm_info_t *out);
 

@@ -490,6 +490,7 @@ struct orc_qwen {
     float *out_norm;
     orc_layer *L;
     int pos_next;
+    int kv_round;
 };
 
 static int get_tensor(orc_gguf *g, const char *name, uint32_t *type, const uint8_t **ptr,
@@ -612,6 +613,48 @@ void orc_qwen_config(const orc_qwen *m, int32_t *c, float *eps, float *base) {
 }
 
 void orc_qwen_reset(orc_qwen *m) { m->pos_next = 0; }
+void orc_qwen_set_kv_round(orc_qwen *m, int mode) { m->kv_round = mode; }
+
+/* binary32 -> binary16 -> binary32 with round-to-nearest-even (finite inputs;
+ * overflow saturates to inf). */
+float orc_round_f16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    uint32_t sign = u & 0x80000000u, ax = u & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return x;
+    float a;
+    memcpy(&a, &ax, 4);
+    float r;
+    if (a >= 65520.0f) r = INFINITY;
+    else if (a < ldexpf(1.0f, -14)) {
+        /* subnormal range: quantum 2^-24 */
+        r = rintf(a * 16777216.0f) / 16777216.0f;
+    } else {
+        int e;
+        frexpf(a, &e);                    /* a in [2^(e-1), 2^e) */
+        float q = ldexpf(1.0f, e - 11);   /* 10 fraction bits */
+        r = rintf(a / q) * q;
+    }
+    uint32_t rb;
+    memcpy(&rb, &r, 4);
+    rb |= sign;
+    memcpy(&r, &rb, 4);
+    return r;
+}
+float orc_round_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    memcpy(&r, &u, 4);
+    return r;
+}
+static void kv_round(float *v, int n, int mode) {
+    if (mode == 1) for (int i = 0; i < n; i++) v[i] = orc_round_f16(v[i]);
+    else if (mode == 2) for (int i = 0; i < n; i++) v[i] = orc_round_bf16(v[i]);
+}
 
 static void gemv(uint32_t t, const uint8_t *w, int rows, int k, const float *x, float *y) {
     orc_gemv_q(t, w, (uint64_t)rows, (uint64_t)k, x, y, 1);
@@ -656,6 +699,8 @@ int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *tr
         orc_rope_neox(k, m->hkv, hd, m->rot, pos, m->base);
         memcpy(y->kcache + (size_t)pos * kd, k, sizeof(float) * kd);
         memcpy(y->vcache + (size_t)pos * kd, v, sizeof(float) * kd);
+        kv_round(y->kcache + (size_t)pos * kd, kd, m->kv_round);
+        kv_round(y->vcache + (size_t)pos * kd, kd, m->kv_round);
         int tokens = pos + 1;
         for (int qh = 0; qh < m->hq; qh++) {
             int kh = qh / group;

@@ -97,6 +97,12 @@ void orc_qwen_config(const orc_qwen *m, int32_t *cfg8, float *eps, float *rope_b
 int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *hidden_trace,
                   float *final_norm);
 void orc_qwen_reset(orc_qwen *m);
+/* Round K/V as they enter the cache: 0 = keep f32 (reference host equations),
+ * 1 = binary16 RNE (the reference CUDA cache, model_ops.rs:1210-1276),
+ * 2 = bfloat16 RNE (the build's default device cache). */
+void orc_qwen_set_kv_round(orc_qwen *m, int mode);
+float orc_round_f16(float x);
+float orc_round_bf16(float x);
 
 #ifdef __cplusplus
 }

@@ -30,6 +30,7 @@ GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 8, 12, 14
 BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
 
 RIBN_OK, RIBN_PENDING = 0, 1
+LOAD_KV_F16 = 1
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -68,7 +69,8 @@ class Info(ctypes.Structure):
                 ("max_decode_tokens", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
                 ("layers", ctypes.c_uint32), ("q_heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
                 ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
-                ("rope_dims", ctypes.c_uint32), ("weight_bytes", ctypes.c_uint64), ("kv_bytes", ctypes.c_uint64)]
+                ("rope_dims", ctypes.c_uint32), ("weight_bytes", ctypes.c_uint64), ("kv_bytes", ctypes.c_uint64),
+                ("kv_f16", ctypes.c_uint32)]
 
 
 class TokenOptions(ctypes.Structure):
@@ -256,8 +258,9 @@ class QwenRocm:
     """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
-                 kv_pages: int = 0, device: int = 0):
-        opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device, 0)
+                 kv_pages: int = 0, device: int = 0, kv_f16: bool = False):
+        opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
+                           LOAD_KV_F16 if kv_f16 else 0)
         h = ctypes.c_void_p()
         err = ctypes.create_string_buffer(_ERR)
         _check(_lib.ribn_rocm_load_gguf(path.encode(), ctypes.byref(opts), ctypes.byref(h), err, _ERR), err)

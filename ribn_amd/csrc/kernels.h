@@ -66,13 +66,14 @@ struct MvSeg {
 struct QkvEpi {
     float* raw;             // [q_dim + 2*kv_dim] projection outputs (+bias)
     float* q_out;           // [hq][hd] after norm + rope
-    uint16_t* kcache;       // layer K cache [pages][hkv][16][hd] bf16
+    uint16_t* kcache;       // layer K cache [pages][hkv][16][hd] (bf16 or f16)
     uint16_t* vcache;
     const float* q_norm;    // optional [hd]
     const float* k_norm;
     uint32_t* counters;     // [hq + hkv] per-head arrival counters (left at 0)
     int32_t hq, hkv, hd, rot;
     float rope_base, eps;
+    int32_t kv_f16;         // cache element: 0 = bf16, 1 = binary16
 };
 
 struct HeadEpi {
@@ -104,6 +105,7 @@ struct AttnArgs {
     const StepCtl* ctl;
     int32_t hq, hkv, hd, n_splits;
     float scale_log2;        // log2(e) / sqrt(hd)
+    int32_t kv_f16;          // cache element: 0 = bf16, 1 = binary16
 };
 
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.

@@ -87,6 +87,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+// KV cache element encode (bf16 RNE, or binary16 RNE like kv_append_f16, model_ops.rs:1210-1276).
+__device__ __forceinline__ uint16_t kv_encode(float f, int f16) {
+    return f16 ? __half_as_ushort(__float2half_rn(f)) : f32_to_bf16(f);
+}
+template <bool F16>
+__device__ __forceinline__ float kv_decode(uint32_t b) {
+    if constexpr (F16) return __half2float(__ushort_as_half((unsigned short)b));
+    else return bf16_to_f32(b);
+}
 
 // Monotone key of model_ops.rs:193-199 packed with the inverted index, so
 // the u64 maximum is the largest logit with the lowest index. NaN -> 0.
@@ -429,7 +438,7 @@ __device__ void head_finish(const MvArgs& a, int kind, int head, float* tmp) {
             r = tmp[i];
         }
         if (kind == 0) qdst[i] = r;
-        else kdst[i] = f32_to_bf16(r);
+        else kdst[i] = kv_encode(r, e.kv_f16);
     }
 }
 
@@ -491,10 +500,10 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
                     const int pos = s->pos, hd = a.qkv.hd;
                     const int page = s->pages[pos / kPageTokens], off = pos % kPageTokens;
                     const int h0 = ra / hd, h1 = rb / hd;
-                    a.qkv.vcache[((size_t)(page * a.qkv.hkv + h0) * kPageTokens + off) * hd + ra % hd] = f32_to_bf16(ya);
+                    a.qkv.vcache[((size_t)(page * a.qkv.hkv + h0) * kPageTokens + off) * hd + ra % hd] = kv_encode(ya, a.qkv.kv_f16);
                     if (has_b)
                         a.qkv.vcache[((size_t)(page * a.qkv.hkv + h1) * kPageTokens + off) * hd + rb % hd] =
-                            f32_to_bf16(yb);
+                            kv_encode(yb, a.qkv.kv_f16);
                 }
                 break;
             }
@@ -568,7 +577,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
 // heads of a KV head share every K/V load. Lanes: LPT = hd/8 lanes per token,
 // 8 dims each. Per split: online softmax in base 2; the last workgroup of a KV
 // head merges the splits by log-sum-exp.
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     constexpr int LPT = HD / 8, TPW = 64 / LPT, NG = kWaves * TPW;
     __shared__ float sm[kWaves][G][HD + 2];
@@ -608,8 +617,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t kw = dword_at(kr, i), vw = dword_at(vr, i);
-            kf[2 * i] = bf16_to_f32(kw & 0xffffu); kf[2 * i + 1] = bf16_to_f32(kw >> 16);
-            vf[2 * i] = bf16_to_f32(vw & 0xffffu); vf[2 * i + 1] = bf16_to_f32(vw >> 16);
+            kf[2 * i] = kv_decode<F16>(kw & 0xffffu); kf[2 * i + 1] = kv_decode<F16>(kw >> 16);
+            vf[2 * i] = kv_decode<F16>(vw & 0xffffu); vf[2 * i + 1] = kv_decode<F16>(vw >> 16);
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -737,19 +746,18 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* logits, u
     }
 }
 
-template <int HD>
+template <int HD, bool F16>
 hipError_t attention_dispatch(const AttnArgs& a, hipStream_t st) {
     dim3 grid(a.n_splits, a.hkv);
-    const int g = a.hq / a.hkv;
-    switch (g) {
-    case 1: attention_kernel<HD, 1><<<grid, kThreads, 0, st>>>(a); break;
-    case 2: attention_kernel<HD, 2><<<grid, kThreads, 0, st>>>(a); break;
-    case 3: attention_kernel<HD, 3><<<grid, kThreads, 0, st>>>(a); break;
-    case 4: attention_kernel<HD, 4><<<grid, kThreads, 0, st>>>(a); break;
-    case 5: attention_kernel<HD, 5><<<grid, kThreads, 0, st>>>(a); break;
-    case 6: attention_kernel<HD, 6><<<grid, kThreads, 0, st>>>(a); break;
-    case 7: attention_kernel<HD, 7><<<grid, kThreads, 0, st>>>(a); break;
-    case 8: attention_kernel<HD, 8><<<grid, kThreads, 0, st>>>(a); break;
+    switch (a.hq / a.hkv) {
+    case 1: attention_kernel<HD, 1, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 2: attention_kernel<HD, 2, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 3: attention_kernel<HD, 3, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 4: attention_kernel<HD, 4, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 5: attention_kernel<HD, 5, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 6: attention_kernel<HD, 6, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 7: attention_kernel<HD, 7, F16><<<grid, kThreads, 0, st>>>(a); break;
+    case 8: attention_kernel<HD, 8, F16><<<grid, kThreads, 0, st>>>(a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -769,8 +777,8 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.n_splits < 1 || a.n_splits > kMaxSplits || a.hq % a.hkv) return hipErrorInvalidValue;
-    if (a.hd == 128) return attention_dispatch<128>(a, st);
-    if (a.hd == 64) return attention_dispatch<64>(a, st);
+    if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
+    if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
     return hipErrorInvalidValue;
 }
 

@@ -67,6 +67,7 @@ struct ribn_rocm_model {
     int H = 0, L = 0, hq = 0, hkv = 0, hd = 0, F = 0, V = 0, rot = 0;
     float eps = 1e-6f, base = 1e6f;
     bool qwen3 = false;
+    bool kv_f16 = false;
     std::string name;
     uint32_t context = 0, max_seqs = 0, max_batch_tokens = 0, kv_pages = 0;
     int max_pages = 0;
@@ -282,6 +283,7 @@ void build_launches(ribn_rocm_model* M) {
         q.qkv.counters = M->counters;
         q.qkv.hq = M->hq; q.qkv.hkv = M->hkv; q.qkv.hd = M->hd; q.qkv.rot = M->rot;
         q.qkv.rope_base = M->base; q.qkv.eps = M->eps;
+        q.qkv.kv_f16 = M->kv_f16 ? 1 : 0;
         M->wg_qkv.push_back(layout_segments(q));
         M->mv_qkv.push_back(q);
 
@@ -333,6 +335,7 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
     at.ctl = M->d_ctl;
     at.hq = M->hq; at.hkv = M->hkv; at.hd = M->hd; at.n_splits = n_splits;
     at.scale_log2 = 1.4426950408889634f / std::sqrt((float)M->hd);
+    at.kv_f16 = M->kv_f16 ? 1 : 0;
     for (int l = 0; l < M->L; l++) {
         if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
         at.kcache = M->layers[l].kc;
@@ -494,6 +497,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     M->kv_pages = o.kv_pages ? o.kv_pages : (uint32_t)(M->max_seqs * M->max_pages);
     if ((int)M->kv_pages < M->max_pages) M->kv_pages = M->max_pages;
     M->device = o.device;
+    M->kv_f16 = (o.flags & RIBN_LOAD_KV_F16) != 0;
     M->name = "ribn-rocm " + arch + " " + std::to_string(M->L) + "x" + std::to_string(M->H);
 
     HIPCHK(hipSetDevice(M->device));
@@ -631,6 +635,7 @@ extern "C" int ribn_rocm_info(const ribn_rocm_model* M, ribn_rocm_info_t* o) {
     o->head_dim = M->hd; o->ffn = M->F; o->vocab = M->V; o->rope_dims = M->rot;
     o->weight_bytes = M->weight_bytes;
     o->kv_bytes = M->kv_bytes;
+    o->kv_f16 = M->kv_f16 ? 1 : 0;
     return RIBN_OK;
 }
 

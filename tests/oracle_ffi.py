@@ -47,6 +47,11 @@ def lib():
         _lib.orc_qwen_config.argtypes = [c.c_void_p, c.c_void_p, c.POINTER(c.c_float), c.POINTER(c.c_float)]
         _lib.orc_qwen_step.argtypes = [c.c_void_p, c.c_uint32, c.c_int, c.c_void_p, c.c_void_p, c.c_void_p]
         _lib.orc_qwen_reset.argtypes = [c.c_void_p]
+        _lib.orc_qwen_set_kv_round.argtypes = [c.c_void_p, c.c_int]
+        _lib.orc_round_f16.restype = c.c_float
+        _lib.orc_round_f16.argtypes = [c.c_float]
+        _lib.orc_round_bf16.restype = c.c_float
+        _lib.orc_round_bf16.argtypes = [c.c_float]
     return _lib
 
 
@@ -147,11 +152,14 @@ class Gguf:
 class QwenOracle:
     """FP32 dense-Qwen forward (oracle.c orc_qwen_*)."""
 
-    def __init__(self, path, max_ctx=512):
+    KV_F32, KV_F16, KV_BF16 = 0, 1, 2
+
+    def __init__(self, path, max_ctx=512, kv_round=0):
         self.h = ctypes.c_void_p()
         rc = lib().orc_qwen_open(path.encode(), max_ctx, ctypes.byref(self.h))
         if rc:
             raise RuntimeError(f"oracle open failed: {rc}")
+        lib().orc_qwen_set_kv_round(self.h, kv_round)
         cfg = (ctypes.c_int32 * 8)()
         eps, base = ctypes.c_float(), ctypes.c_float()
         lib().orc_qwen_config(self.h, cfg, ctypes.byref(eps), ctypes.byref(base))

@@ -182,3 +182,16 @@ def test_gemv_matches_fp64_dot_of_dequantized():
         ref = w @ x.astype(np.float64)
         np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
         assert np.array_equal(orc.gemv(t, blocks, rows, k, x, threads=3), y)   # threads do not change rows
+
+
+def test_kv_rounding_helpers():
+    """orc_round_f16 vs numpy binary16 casts; orc_round_bf16 vs torch bfloat16 casts (both RNE)."""
+    import torch
+    lib = orc.lib()
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.standard_normal(20000) * s for s in (1e-7, 1e-5, 1e-2, 1, 1e3, 6e4)]).astype(np.float32)
+    x = np.concatenate([x, np.float32([65504, 65519.9, 65520, -65520, 2 ** -24, 2 ** -25, 3 * 2 ** -26, 0.0])])
+    f16 = np.array([lib.orc_round_f16(float(v)) for v in x], np.float32)
+    np.testing.assert_array_equal(f16, x.astype(np.float16).astype(np.float32))
+    bf = np.array([lib.orc_round_bf16(float(v)) for v in x], np.float32)
+    np.testing.assert_array_equal(bf, torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy())
