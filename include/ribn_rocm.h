@@ -54,13 +54,13 @@ typedef struct {
     uint32_t context_tokens;   /* per-sequence limit (0 -> min(GGUF context_length, 4096)) */
     uint32_t max_sequences;    /* 0 -> 8 */
     uint32_t max_batch_tokens; /* 0 -> 2048 */
-    uint32_t kv_pages;         /* 16-token BF16 pages in the pool (0 -> max_sequences*context/16) */
+    uint32_t kv_pages;         /* 16-token KV pages in the pool (0 -> max_sequences*context/16) */
     int32_t device;            /* HIP device ordinal */
     uint32_t flags;            /* RIBN_LOAD_* bits */
 } ribn_rocm_load_options;
-/* KV cache in binary16 (the reference CUDA cache type, nvidia/src/model_ops.rs:1258)
- * instead of the default bfloat16. */
-#define RIBN_LOAD_KV_F16 1u
+/* KV cache in bfloat16 instead of the default binary16 (binary16 is the reference
+ * CUDA cache type, kv_append_f16 nvidia/src/model_ops.rs:1258-1276). */
+#define RIBN_LOAD_KV_BF16 1u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);

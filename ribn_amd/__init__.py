@@ -30,7 +30,7 @@ GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 8, 12, 14
 BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}
 
 RIBN_OK, RIBN_PENDING = 0, 1
-LOAD_KV_F16 = 1
+LOAD_KV_BF16 = 1
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -258,9 +258,11 @@ class QwenRocm:
     """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
-                 kv_pages: int = 0, device: int = 0, kv_f16: bool = False):
+                 kv_pages: int = 0, device: int = 0, kv: str = "f16"):
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
-                           LOAD_KV_F16 if kv_f16 else 0)
+                           LOAD_KV_BF16 if kv == "bf16" else 0)
+        if kv not in ("f16", "bf16"):
+            raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()
         err = ctypes.create_string_buffer(_ERR)
         _check(_lib.ribn_rocm_load_gguf(path.encode(), ctypes.byref(opts), ctypes.byref(h), err, _ERR), err)

@@ -497,7 +497,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     M->kv_pages = o.kv_pages ? o.kv_pages : (uint32_t)(M->max_seqs * M->max_pages);
     if ((int)M->kv_pages < M->max_pages) M->kv_pages = M->max_pages;
     M->device = o.device;
-    M->kv_f16 = (o.flags & RIBN_LOAD_KV_F16) != 0;
+    M->kv_f16 = (o.flags & RIBN_LOAD_KV_BF16) == 0;
     M->name = "ribn-rocm " + arch + " " + std::to_string(M->L) + "x" + std::to_string(M->H);
 
     HIPCHK(hipSetDevice(M->device));
