@@ -131,7 +131,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, fp16-staged activations, fp32 accumulate, bf16 KV",
+        "dtype": "q4_k/q6_k weights, fp16-staged activations, fp32 accumulate, f16 KV",
         "data": "synthetic (seeded N(0,0.02) weights quantized to GGUF Q4_K_M; random prompt)",
         "config": {"workload": "qwen3-8b-shape Q4_K_M bs1 greedy decode (BASELINE configs[2])",
                    "prompt": args.prompt, "decode_tokens": args.steps, "layers": info.layers,
