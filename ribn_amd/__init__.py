@@ -350,9 +350,9 @@ class QwenRocm:
                    None if lg is None else _ptr(lg, _f32p), None if hd is None else _ptr(hd, _f32p))
         return am, lg, hd
 
-    def bench_kernel(self, which: int, iters: int = 50):
+    def bench_kernel(self, which: int, iters: int = 50, ctx: int = 0):
         ms = ctypes.c_double()
-        nbytes = ctypes.c_uint64()
+        nbytes = ctypes.c_uint64(ctx)
         self._call(_lib.ribn_rocm_bench_model_kernel, which, iters, ctypes.byref(ms), ctypes.byref(nbytes))
         return ms.value, nbytes.value
 

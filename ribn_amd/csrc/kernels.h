@@ -7,7 +7,8 @@
 namespace ribn {
 
 constexpr int kPageTokens = 16;   // KV page size (crates/qwen/src/gguf.rs:16)
-constexpr int kMaxSplits = 512;   // split-K limit of decode attention
+constexpr int kMaxSplits = 128;   // split-K limit of decode attention
+constexpr int kMaxSplitTokens = 512;   // positions one attention workgroup covers
 
 // A quantized matrix after load-time re-tiling: `rows` output rows of `k`
 // inputs, GGML row n = input-contiguous. Each GGML block is split into
@@ -50,8 +51,7 @@ enum MvMode : int32_t {
     MV_STORE = 0,   // out[row] = y (+ bias)
     MV_ADD = 1,     // out[row] += y   (residual epilogue)
     MV_SILU = 2,    // pair (gate, up): out[j] = silu(gate_j) * up_j
-    MV_QKV = 3,     // q/k/v projection with head epilogue (norm, rope, KV append)
-    MV_HEAD = 4,    // vocab logits + greedy argmax
+    MV_HEAD = 3,    // vocab logits + greedy argmax (token written to the sequence)
 };
 
 struct MvSeg {
@@ -60,20 +60,7 @@ struct MvSeg {
     float* out;
     const float* bias;   // optional per-row bias
     int32_t wg_begin;    // first workgroup of this segment
-    int32_t kind;        // MV_QKV: 0 = q, 1 = k, 2 = v
-};
-
-struct QkvEpi {
-    float* raw;             // [q_dim + 2*kv_dim] projection outputs (+bias)
-    float* q_out;           // [hq][hd] after norm + rope
-    uint16_t* kcache;       // layer K cache [pages][hkv][16][hd] (bf16 or f16)
-    uint16_t* vcache;
-    const float* q_norm;    // optional [hd]
-    const float* k_norm;
-    uint32_t* counters;     // [hq + hkv] per-head arrival counters (left at 0)
-    int32_t hq, hkv, hd, rot;
-    float rope_base, eps;
-    int32_t kv_f16;         // cache element: 0 = bf16, 1 = binary16
+    int32_t pad;
 };
 
 struct HeadEpi {
@@ -81,6 +68,8 @@ struct HeadEpi {
     uint32_t* counter;      // arrival counter (left at 0)
 };
 
+// One launch of the fused dequant-matvec. Segments 0 and 1 share the value
+// type `type_a`; segment 2 may use `type_b` (QKV: attn_v is Q6_K in Q4_K_M).
 struct MvArgs {
     const float* x;          // input vector [k]
     const float* norm_w;     // optional RMSNorm weight: x := rms_norm(x) * w
@@ -89,23 +78,38 @@ struct MvArgs {
     int32_t mode;
     int32_t nseg;
     int32_t items_per_wave;  // item = 2 weight rows (or one gate/up pair)
+    uint32_t type_a, type_b;
     MvSeg seg[3];
-    QkvEpi qkv;
     HeadEpi head;
     const StepCtl* ctl;
 };
 
+// Per-step rotary table: cos/sin of theta_p = pos * base^(-2p/rot) for the
+// active sequence's position, written by the embedding kernel.
+struct EmbedArgs {
+    QMat w;
+    int32_t hidden;
+    float* h;
+    const StepCtl* ctl;
+    const float* inv_freq;   // [rot/2] base^(-2p/rot), f32 (powf on the host)
+    float* rope;             // [rot]: cos[0..rot/2), sin[rot/2..rot)
+    int32_t half_rot;
+};
+
 struct AttnArgs {
-    const float* q;          // [hq][hd] (normed, roped)
-    const uint16_t* kcache;  // [pages][hkv][16][hd] bf16
-    const uint16_t* vcache;
-    float* part;             // [hq][n_splits][hd + 2]
+    const float* raw;        // QKV projection output [hq*hd | hkv*hd | hkv*hd]
+    const float* q_norm;     // optional per-head RMSNorm weights [hd]
+    const float* k_norm;
+    const float* rope;       // EmbedArgs::rope
+    uint16_t* kcache;        // [pages][hkv][16][hd] (bf16 or f16)
+    uint16_t* vcache;
+    float* part;             // split partials [hkv][n_splits][G*hd + 2*G]
     uint32_t* counters;      // [hkv] (left at 0)
     float* out;              // [hq][hd]
     const StepCtl* ctl;
-    int32_t hq, hkv, hd, n_splits;
+    int32_t hq, hkv, hd, rot, n_splits, kv_f16;
+    float eps;
     float scale_log2;        // log2(e) / sqrt(hd)
-    int32_t kv_f16;          // cache element: 0 = bf16, 1 = binary16
 };
 
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.
@@ -113,7 +117,7 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);
 int matvec_rows_per_wg(const MvArgs& a);
 size_t matvec_lds_bytes(int k);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
-hipError_t launch_embed(const QMat& w, int hidden, float* h, const StepCtl* ctl, hipStream_t stream);
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t stream);
 hipError_t launch_dequant(const QMat& w, float* out, hipStream_t stream);
 hipError_t launch_argmax(const float* logits, uint32_t n, uint64_t* partial, uint32_t* counter,

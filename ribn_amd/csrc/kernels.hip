@@ -11,9 +11,9 @@
 //    bits) and meet x in v_dot2_f32_f16 with fp32 accumulation; the constant
 //    1024 (and the Q6_K/Q8_0 offsets) is removed with the 16-element sums,
 //    and the Q4_K minimum term uses the same sums;
-//  * RMSNorm is a workgroup prologue; residual add, SwiGLU, q/k head norm +
-//    NeoX rope + BF16 KV append, and the vocab argmax are epilogues, so one
-//    layer is 5 launches.
+//  * RMSNorm is a workgroup prologue; residual add, SwiGLU and the vocab argmax
+//    are epilogues; q/k head norm, NeoX rope and the KV append live in the
+//    attention prologue, so one layer is 5 launches.
 // Reference semantics followed: gguf_gemv (nvidia/src/qwen_reference.rs:31-40),
 // rms_norm_raw (:550-556), rope (:406-425), attention (:431-461), ffn (:529-539),
 // argmax (nvidia/src/model_ops.rs:203-260), dequant (gguf/src/lib.rs:577-649).
@@ -30,7 +30,6 @@ typedef unsigned u4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kTailBytes = 2048;   // LDS tail: reductions + head-epilogue staging
 
 __device__ __forceinline__ u4_t ld_nt16(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
@@ -106,8 +105,37 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
     return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
 }
 
-__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Cross-workgroup hand-off inside one kernel. The eight XCD-local L2 caches are
+// not coherent with each other and an agent-scope fence writes back or
+// invalidates a whole L2 (buffer_wbl2 / buffer_inv), which costs tens of
+// microseconds across a grid. Instead, handed-off values move with agent-scope
+// atomic stores and loads (coherent per access), each wave waits until its
+// stores are acknowledged before its workgroup's arrival is counted, and the
+// arrival counter is a device-scope atomic.
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Count this workgroup's arrival; true in the last of `total` workgroups,
+// which also rearms the counter for the next launch.
+__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t total) {
+    __shared__ int last;
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = atomicAdd(ctr, 1u);
+        last = old == total - 1;
+        if (last) st_agent(ctr, 0u);
+    }
+    __syncthreads();
+    return last != 0;
+}
 
 // ---------------------------------------------------------------------------
 // Exact dequantization of one element, bit-identical to dequantize_block
@@ -161,12 +189,20 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(QMat w, float* out) {
 }
 
 // Token embedding: one row of token_embd dequantized exactly
-// (q4_k_embedding, kernels/quantized/q4_k.cu:1; reference decode.rs:577-582).
-__global__ __launch_bounds__(kThreads) void embed_kernel(QMat w, int hidden, float* h, const StepCtl* ctl) {
-    const SeqState* s = ctl->seq;
-    uint32_t tok = s->tokens[s->pos];
-    int e = blockIdx.x * kThreads + threadIdx.x;
-    if (e < hidden) h[e] = deq_elem(w, tok, (uint32_t)e);
+// (q4_k_embedding, kernels/quantized/q4_k.cu:1; reference decode.rs:577-582),
+// plus the step's rotary table: theta_p = pos * base^(-2p/rot) in f32 and its
+// sin/cos (qwen_reference.rs:406-425), shared by every layer of the step.
+__global__ __launch_bounds__(kThreads) void embed_kernel(EmbedArgs a) {
+    const SeqState* s = a.ctl->seq;
+    const int pos = s->pos;
+    const uint32_t tok = s->tokens[pos];
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    if (e < a.hidden) a.h[e] = deq_elem(a.w, tok, (uint32_t)e);
+    if (blockIdx.x == 0 && (int)threadIdx.x < a.half_rot) {
+        const float theta = (float)pos * a.inv_freq[threadIdx.x];
+        a.rope[threadIdx.x] = cosf(theta);
+        a.rope[a.half_rot + threadIdx.x] = sinf(theta);
+    }
 }
 
 __global__ void advance_kernel(const StepCtl* ctl) {
@@ -174,24 +210,36 @@ __global__ void advance_kernel(const StepCtl* ctl) {
 }
 
 // ---------------------------------------------------------------------------
-// Matvec input staging: x (optionally RMS-normalised, rms_norm model_ops.rs:108)
-// -> fp16 in LDS scaled by 2^e so that max|x| lies in [2^14, 2^15), plus fp32
-// sums of each 16 staged values. Returns 2^-e, the output scale.
-__device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* red) {
+// Matvec input staging: x (optionally RMS-normalised, rms_norm model_ops.rs:108:
+// x * (1/sqrt(sum/n + eps)) * w) -> fp16 in LDS scaled by 2^e so that max|x|
+// lies in [2^14, 2^15), plus fp32 sums of each 16 staged values. Inputs up to
+// kStageF32 elements are read once (kept as fp32 in LDS between the statistics
+// and the conversion); longer ones are read twice. Returns 2^-e.
+constexpr int kStageF32 = 8192;
+
+// LDS layout of the matvec: [k] fp16 | [k/16] fp32 sums | 64 fp32 reduction
+// slots | (k <= kStageF32) [k] fp32 staging; 16-byte aligned pieces.
+__host__ __device__ constexpr size_t mv_red_offset(int k) {
+    return ((size_t)k * 2 + (size_t)(k / 16) * 4 + 15) / 16 * 16;
+}
+
+__device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* xf, float* red) {
     const int k = a.k, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
     const bool norm = a.norm_w != nullptr;
+    const bool keep = k <= kStageF32;
+    float4* xf4 = reinterpret_cast<float4*>(xf);
     float ss = 0.f, am = 0.f;
     for (int i = tid; i < k / 4; i += kThreads) {
         float4 v = x4[i];
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         if (norm) {
-            float4 w = w4[i];
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x * w.x), fabsf(v.y * w.y)), fmaxf(fabsf(v.z * w.z), fabsf(v.w * w.w))));
-        } else {
-            am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            const float4 w = w4[i];
+            v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;   // x*w; inv is applied below
         }
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        if (keep) xf4[i] = v;
     }
     ss = wave_sum(ss);
     am = wave_max(am);
@@ -201,7 +249,7 @@ __device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* red) {
 #pragma unroll
     for (int i = 0; i < kWaves; i++) { ss += red[i]; am = fmaxf(am, red[kWaves + i]); }
     const float inv = norm ? 1.0f / sqrtf(ss / (float)k + a.eps) : 1.0f;
-    float amax = am * inv * 1.0001f;
+    const float amax = am * inv * 1.0001f;
     int ex = 0;
     if (amax > 0.f && amax < 3.0e38f) frexpf(amax, &ex);
     ex = min(max(15 - ex, -100), 100);
@@ -210,24 +258,23 @@ __device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* red) {
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float4 t = x4[g * 4 + j];
-            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
-        }
-        if (norm) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float4 t = w4[g * 4 + j];
-                v[4 * j] = v[4 * j] * inv * t.x;
-                v[4 * j + 1] = v[4 * j + 1] * inv * t.y;
-                v[4 * j + 2] = v[4 * j + 2] * inv * t.z;
-                v[4 * j + 3] = v[4 * j + 3] * inv * t.w;
+            float4 t;
+            if (keep) {
+                t = xf4[g * 4 + j];
+            } else {
+                t = x4[g * 4 + j];
+                if (norm) {
+                    const float4 w = w4[g * 4 + j];
+                    t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
+                }
             }
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
         }
         float sum = 0.f;
         _Float16 hv[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            hv[j] = (_Float16)(v[j] * scale);
+            hv[j] = (_Float16)(v[j] * inv * scale);
             sum += (float)hv[j];
         }
         u4_t* dst = reinterpret_cast<u4_t*>(xs + g * 16);
@@ -376,78 +423,17 @@ __device__ __forceinline__ void rows2(const QMat& wa, size_t ra, const QMat& wb,
     acc_b = wave_sum(b0 + b1);
 }
 
-__device__ __forceinline__ void rows2_any(const QMat& wa, size_t ra, const QMat& wb, size_t rb, const u4_t* xs4,
-                                          const float* gs, float& ya, float& yb) {
-    switch (wa.type) {
-    case 12: rows2<12>(wa, ra, wb, rb, xs4, gs, ya, yb); break;
-    case 14: rows2<14>(wa, ra, wb, rb, xs4, gs, ya, yb); break;
-    default: rows2<8>(wa, ra, wb, rb, xs4, gs, ya, yb); break;
-    }
-}
-
-// q/k head epilogue, run by wave 0 of the last workgroup of a head: per-head
-// RMSNorm (qwen_reference.rs:382-400, dense Qwen3: stride hd) and NeoX rope
-// (:406-425) with theta = pos * base^(-2p/rot); q -> q_out, k -> BF16 cache.
-__device__ void head_finish(const MvArgs& a, int kind, int head, float* tmp) {
-    const QkvEpi& e = a.qkv;
-    const int hd = e.hd, lane = threadIdx.x & 63;
-    const SeqState* s = a.ctl->seq;
-    const int pos = s->pos;
-    const float* src = e.raw + (kind == 0 ? head * hd : e.hq * hd + head * hd);
-    const float* nw = kind == 0 ? e.q_norm : e.k_norm;
-    float v[4];
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = lane + 64 * j;
-        v[j] = i < hd ? __builtin_nontemporal_load(src + i) : 0.f;
-        ss += v[j] * v[j];
-    }
-    if (nw) {
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)hd + e.eps);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = lane + 64 * j;
-            if (i < hd) v[j] = v[j] * inv * nw[i];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = lane + 64 * j;
-        if (i < hd) tmp[i] = v[j];
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int half = e.rot / 2;
-    const int page = s->pages[pos / kPageTokens], off = pos % kPageTokens;
-    uint16_t* kdst = e.kcache + ((size_t)(page * e.hkv + head) * kPageTokens + off) * hd;
-    float* qdst = e.q_out + head * hd;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = lane + 64 * j;
-        if (i >= hd) continue;
-        float r;
-        if (i < e.rot) {
-            const int p = i < half ? i : i - half;
-            const float theta = (float)pos * powf(e.rope_base, -(2.0f * (float)p) / (float)e.rot);
-            const float sn = sinf(theta), cs = cosf(theta);
-            const float x0 = tmp[p], x1 = tmp[p + half];
-            r = i < half ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
-        } else {
-            r = tmp[i];
-        }
-        if (kind == 0) qdst[i] = r;
-        else kdst[i] = kv_encode(r, e.kv_f16);
-    }
-}
-
+// Fused dequant-matvec (gguf_gemv qwen_reference.rs:31-40; q*_gemv_warp
+// kernels/quantized/q4_k.cu:103, q6_k.cu:45, q8_0.cu:27). Each wave computes
+// two rows per item (or a gate/up pair); rows of a workgroup are contiguous.
+template <int TA, int TB, int MODE>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     _Float16* xs = reinterpret_cast<_Float16*>(lds);
     float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
-    float* tail = gs + a.k / 16;
-    const float oscale = stage_x(a, xs, gs, tail);
+    float* red = reinterpret_cast<float*>(lds + mv_red_offset(a.k));
+    float* xf = red + 64;
+    const float oscale = stage_x(a, xs, gs, xf, red);
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
 
     const int wg = blockIdx.x;
@@ -458,8 +444,8 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     const int lwg = wg - sg.wg_begin;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ipw = a.items_per_wave;
-    const bool pair = a.mode == MV_SILU;
-    const int rows_per_item = pair ? 1 : 2;
+    constexpr bool pair = MODE == MV_SILU;
+    constexpr int rows_per_item = pair ? 1 : 2;
     const int n_rows = (int)sg.w.rows;
     uint64_t best = 0ull;
 
@@ -469,7 +455,8 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
         if (ra >= n_rows) break;
         const int rb = pair ? ra : min(ra + 1, n_rows - 1);
         float ya, yb;
-        rows2_any(sg.w, (size_t)ra, pair ? sg.w2 : sg.w, (size_t)rb, xs4, gs, ya, yb);
+        if (si == 2 && TB != TA) rows2<TB>(sg.w, (size_t)ra, sg.w, (size_t)rb, xs4, gs, ya, yb);
+        else rows2<TA>(sg.w, (size_t)ra, pair ? sg.w2 : sg.w, (size_t)rb, xs4, gs, ya, yb);
         ya *= oscale;
         yb *= oscale;
         if (lane == 0) {
@@ -478,81 +465,38 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
                 ya += sg.bias[ra];
                 if (has_b) yb += sg.bias[rb];
             }
-            switch (a.mode) {
-            case MV_ADD:
+            if constexpr (MODE == MV_ADD) {
                 sg.out[ra] += ya;
                 if (has_b) sg.out[rb] += yb;
-                break;
-            case MV_SILU:
+            } else if constexpr (MODE == MV_SILU) {
                 sg.out[ra] = ya / (1.0f + expf(-ya)) * yb;
-                break;
-            case MV_HEAD:
+            } else {
                 sg.out[ra] = ya;
                 if (has_b) sg.out[rb] = yb;
-                best = max(best, argmax_key(ya, (uint32_t)ra));
-                if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
-                break;
-            default:
-                sg.out[ra] = ya;
-                if (has_b) sg.out[rb] = yb;
-                if (a.mode == MV_QKV && sg.kind == 2) {
-                    const SeqState* s = a.ctl->seq;
-                    const int pos = s->pos, hd = a.qkv.hd;
-                    const int page = s->pages[pos / kPageTokens], off = pos % kPageTokens;
-                    const int h0 = ra / hd, h1 = rb / hd;
-                    a.qkv.vcache[((size_t)(page * a.qkv.hkv + h0) * kPageTokens + off) * hd + ra % hd] = kv_encode(ya, a.qkv.kv_f16);
-                    if (has_b)
-                        a.qkv.vcache[((size_t)(page * a.qkv.hkv + h1) * kPageTokens + off) * hd + rb % hd] =
-                            kv_encode(yb, a.qkv.kv_f16);
+                if constexpr (MODE == MV_HEAD) {
+                    best = max(best, argmax_key(ya, (uint32_t)ra));
+                    if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
                 }
-                break;
             }
         }
     }
 
-    if (a.mode == MV_QKV && sg.kind < 2) {
-        // Last workgroup of a head finishes it (rows per workgroup divide hd).
-        __shared__ int is_last;
-        const int rows_wg = ipw * kWaves * 2;
-        const int head = (lwg * rows_wg) / a.qkv.hd;
-        const int per_head = a.qkv.hd / rows_wg;
-        uint32_t* ctr = a.qkv.counters + (sg.kind == 0 ? head : a.qkv.hq + head);
-        fence_release();   // every wave's row stores complete before the arrival
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t old = atomicAdd(ctr, 1u);
-            is_last = (old == (uint32_t)per_head - 1);
-        }
-        __syncthreads();
-        if (is_last) {
-            fence_acquire();
-            if (wave == 0) head_finish(a, sg.kind, head, tail + 64);
-            if (threadIdx.x == 0) *ctr = 0u;
-        }
-    } else if (a.mode == MV_HEAD) {
+    if constexpr (MODE == MV_HEAD) {
+        // Greedy token: first maximum over the vocabulary, NaN skipped (model_ops.rs:203-260).
         __shared__ uint64_t wbest[kWaves];
-        __shared__ int is_last;
         if (lane == 0) wbest[wave] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
             uint64_t b = wbest[0];
             for (int i = 1; i < kWaves; i++) b = max(b, wbest[i]);
-            a.head.partial[wg] = b;
-            fence_release();
-            const uint32_t old = atomicAdd(a.head.counter, 1u);
-            is_last = (old == gridDim.x - 1);
+            st_agent(a.head.partial + wg, b);
         }
-        __syncthreads();
-        if (is_last) {
-            fence_acquire();
+        if (arrive_last(a.head.counter, gridDim.x)) {
             uint64_t b = 0ull;
-            for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads)
-                b = max(b, __builtin_nontemporal_load(a.head.partial + i));
+            for (int i = threadIdx.x; i < (int)gridDim.x; i += kThreads) b = max(b, ld_agent(a.head.partial + i));
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const uint64_t other = __shfl_xor(b, o);
-                b = max(b, other);
-            }
+            for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
+            __syncthreads();
             if (lane == 0) wbest[wave] = b;
             __syncthreads();
             if (threadIdx.x == 0) {
@@ -564,158 +508,237 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
                 if (pos + 1 <= s->max_ctx) s->tokens[pos + 1] = tok;
                 s->last_token = tok;
                 s->pos = pos + 1;
-                *a.head.counter = 0u;
             }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// GQA decode attention over the paged BF16 cache with split-K over the
-// context (attn_score_gqa_paged, model_ops.rs:442-590; host equations
-// qwen_reference.rs:431-461). Workgroup (split, kv head); the G = hq/hkv query
-// heads of a KV head share every K/V load. Lanes: LPT = hd/8 lanes per token,
-// 8 dims each. Per split: online softmax in base 2; the last workgroup of a KV
-// head merges the splits by log-sum-exp.
+// GQA decode attention over the paged KV cache with split-K over the context
+// (attn_score_gqa_paged, model_ops.rs:442-590; host equations
+// qwen_reference.rs:368-461, dense Qwen3: no gate). Workgroup (split, kv head);
+// the G = hq/hkv query heads of a KV head share every K/V load.
+//  prologue: q (G heads) and k of the current token get per-head RMSNorm
+//            (qwen_reference.rs:382-400) and NeoX rope from the step table; the
+//            workgroup whose split holds the current position appends k, v to
+//            the cache (kv_append_f16, model_ops.rs:1258);
+//  phase 1:  one token per lane, full-row q.k for the G heads -> LDS;
+//  phase 2:  exact softmax statistics of the split (max, sum of exp2);
+//  phase 3:  P.V with 16-byte V loads, lanes over (dims, token slices);
+//  merge:    splits are combined by log-sum-exp in the last workgroup.
+// Every key and value, including the current token's, is read back at the
+// cache's precision, as the reference reads its F16 cache.
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
-    constexpr int LPT = HD / 8, TPW = 64 / LPT, NG = kWaves * TPW;
-    __shared__ float sm[kWaves][G][HD + 2];
-    __shared__ int is_last;
+    constexpr int CH = HD / 8;                 // 16-byte chunks per row
+    constexpr int NS = kThreads / CH;          // token slices in phase 3
+    constexpr int REC = G * HD + 2 * G;        // partial record floats
+    __shared__ float buf[G + 2][HD];           // q heads, k, v of the current token
+    __shared__ float sc[G][kMaxSplitTokens];   // scores, then probabilities
+    __shared__ float red[NS][HD];              // phase-3 reduction
+    __shared__ float stat[2][G];               // per-head max, sum
+    __shared__ int pg[kMaxSplitTokens / kPageTokens];
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int tg = wave * TPW + lane / LPT, dl = lane % LPT;
     const SeqState* s = a.ctl->seq;
-    const int ctx = s->pos + 1;
+    const int pos = s->pos, ctx = pos + 1;
     int per = (ctx + a.n_splits - 1) / a.n_splits;
     per = (per + kPageTokens - 1) / kPageTokens * kPageTokens;
-    const int t0 = split * per, t1 = min(ctx, t0 + per);
-
-    float q[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float* qp = a.q + (size_t)(kvh * G + g) * HD + dl * 8;
-        const float4 q0 = *reinterpret_cast<const float4*>(qp), q1 = *reinterpret_cast<const float4*>(qp + 4);
-        q[g][0] = q0.x * a.scale_log2; q[g][1] = q0.y * a.scale_log2;
-        q[g][2] = q0.z * a.scale_log2; q[g][3] = q0.w * a.scale_log2;
-        q[g][4] = q1.x * a.scale_log2; q[g][5] = q1.y * a.scale_log2;
-        q[g][6] = q1.z * a.scale_log2; q[g][7] = q1.w * a.scale_log2;
+    if (per > kMaxSplitTokens) {
+        // A split wider than the LDS tiles: the host picked too few splits for
+        // this context. Poison the output instead of touching memory.
+        if (split == 0)
+            for (int i = tid; i < G * HD; i += kThreads) a.out[(size_t)kvh * G * HD + i] = __uint_as_float(0x7fc00000u);
+        return;
     }
-    float m[G], l[G], o[G][8];
+    const int t0 = split * per, t1 = min(ctx, t0 + per), n = max(0, t1 - t0);
+    const int qd = a.hq * HD, kd = a.hkv * HD;
+
+    // -- prologue: raw q/k/v -> LDS, per-head norm, rope
+    for (int i = tid; i < (G + 2) * HD; i += kThreads) {
+        const int r = i / HD, d = i % HD;
+        const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
+                                 : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
+        buf[r][d] = src[d];
+    }
+    for (int i = tid; i < n; i += kThreads) {
+        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = s->pages[(t0 + i) / kPageTokens];
+    }
+    __syncthreads();
+    if (a.q_norm) {
+        for (int r = wave; r <= G; r += kWaves) {
+            const float* nw = r < G ? a.q_norm : a.k_norm;
+            float ss = 0.f;
+            for (int d = lane; d < HD; d += 64) ss += buf[r][d] * buf[r][d];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            for (int d = lane; d < HD; d += 64) buf[r][d] = buf[r][d] * inv * nw[d];
+        }
+        __syncthreads();
+    }
+    const int half = a.rot / 2;
+    for (int i = tid; i < (G + 1) * half; i += kThreads) {
+        const int r = i / half, p = i % half;
+        const float c = a.rope[p], sn = a.rope[half + p];
+        const float x0 = buf[r][p], x1 = buf[r][p + half];
+        buf[r][p] = x0 * c - x1 * sn;
+        buf[r][p + half] = x0 * sn + x1 * c;
+    }
+    __syncthreads();
+    const bool owner = t0 <= pos && pos < t1;
+    if (tid < 2 * HD) {
+        // the current token at cache precision (and appended by the owner)
+        const int r = G + tid / HD, d = tid % HD;
+        const uint16_t e = kv_encode(buf[r][d], F16 ? 1 : 0);
+        if (owner) {
+            const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
+            uint16_t* dst = (r == G ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
+            dst[d] = e;
+        }
+        buf[r][d] = kv_decode<F16>(e);
+    }
+    __syncthreads();
+
+    // -- phase 1: scores (log2 domain)
+    for (int tl = tid; tl < n; tl += kThreads) {
+        const int t = t0 + tl;
+        float acc[G];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        m[g] = -INFINITY; l[g] = 0.f;
+        for (int g = 0; g < G; g++) acc[g] = 0.f;
+        if (t == pos) {
+            for (int d = 0; d < HD; d++) {
+                const float kv = buf[G][d];
+#pragma unroll
+                for (int g = 0; g < G; g++) acc[g] = fmaf(buf[g][d], kv, acc[g]);
+            }
+        } else {
+            const uint16_t* kr = a.kcache + ((size_t)(pg[tl / kPageTokens] * a.hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD;
+#pragma unroll 1
+            for (int c0 = 0; c0 < CH; c0 += 4) {
+                u4_t kw[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) kw[c] = *reinterpret_cast<const u4_t*>(kr + (c0 + c) * 8);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t w = dword_at(kw[c], i);
+                        const float k0 = kv_decode<F16>(w & 0xffffu), k1 = kv_decode<F16>(w >> 16);
+                        const int d = (c0 + c) * 8 + 2 * i;
+#pragma unroll
+                        for (int g = 0; g < G; g++) {
+                            const float2 qq = *reinterpret_cast<const float2*>(&buf[g][d]);
+                            acc[g] = fmaf(qq.x, k0, acc[g]);
+                            acc[g] = fmaf(qq.y, k1, acc[g]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) sc[g][tl] = acc[g] * a.scale_log2;
+    }
+    __syncthreads();
+
+    // -- phase 2: softmax statistics per head
+    for (int g = wave; g < G; g += kWaves) {
+        float m = -INFINITY;
+        for (int tl = lane; tl < n; tl += 64) m = fmaxf(m, sc[g][tl]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int tl = lane; tl < n; tl += 64) {
+            const float p = exp2f(sc[g][tl] - m);
+            sc[g][tl] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { stat[0][g] = m; stat[1][g] = l; }
+    }
+    __syncthreads();
+
+    // -- phase 3: o[g] = sum_t p[g][t] v[t]
+    const int ch = tid % CH, sl = tid / CH;
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) o[g][i] = 0.f;
-    }
-    for (int t = t0 + tg; t < t1; t += NG) {
-        const int page = s->pages[t / kPageTokens];
-        const size_t base = ((size_t)(page * a.hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD + dl * 8;
-        const u4_t kr = *reinterpret_cast<const u4_t*>(a.kcache + base);
-        const u4_t vr = *reinterpret_cast<const u4_t*>(a.vcache + base);
-        float kf[8], vf[8];
+    for (int tl = sl; tl < n; tl += NS) {
+        const int t = t0 + tl;
+        float v[8];
+        if (t == pos) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t kw = dword_at(kr, i), vw = dword_at(vr, i);
-            kf[2 * i] = kv_decode<F16>(kw & 0xffffu); kf[2 * i + 1] = kv_decode<F16>(kw >> 16);
-            vf[2 * i] = kv_decode<F16>(vw & 0xffffu); vf[2 * i + 1] = kv_decode<F16>(vw >> 16);
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float sc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) sc = fmaf(q[g][i], kf[i], sc);
-#pragma unroll
-            for (int off = 1; off < LPT; off <<= 1) sc += __shfl_xor(sc, off);
-            const float mn = fmaxf(m[g], sc);
-            const float corr = exp2f(m[g] - mn), p = exp2f(sc - mn);
-            l[g] = l[g] * corr + p;
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[g][i] = fmaf(o[g][i], corr, p * vf[i]);
-            m[g] = mn;
-        }
-    }
-    // merge the token groups of a wave
-#pragma unroll
-    for (int off = LPT; off < 64; off <<= 1) {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float mo = __shfl_xor(m[g], off), lo = __shfl_xor(l[g], off);
-            const float mn = fmaxf(m[g], mo);
-            const float ca = mn == -INFINITY ? 0.f : exp2f(m[g] - mn);
-            const float cb = mn == -INFINITY ? 0.f : exp2f(mo - mn);
-            l[g] = l[g] * ca + lo * cb;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float oo = __shfl_xor(o[g][i], off);
-                o[g][i] = o[g][i] * ca + oo * cb;
-            }
-            m[g] = mn;
-        }
-    }
-    if (lane < LPT) {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) sm[wave][g][dl * 8 + i] = o[g][i];
-            if (dl == 0) { sm[wave][g][HD] = m[g]; sm[wave][g][HD + 1] = l[g]; }
-        }
-    }
-    __syncthreads();
-    const bool direct = a.n_splits == 1;
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD, d = idx % HD;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) mx = fmaxf(mx, sm[w][g][HD]);
-        float lt = 0.f, ot = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            const float c = mx == -INFINITY ? 0.f : exp2f(sm[w][g][HD] - mx);
-            lt += sm[w][g][HD + 1] * c;
-            ot += sm[w][g][d] * c;
-        }
-        const int qh = kvh * G + g;
-        if (direct) {
-            a.out[qh * HD + d] = ot / lt;
+            for (int i = 0; i < 8; i++) v[i] = buf[G + 1][ch * 8 + i];
         } else {
-            float* p = a.part + ((size_t)qh * a.n_splits + split) * (HD + 2);
-            p[d] = ot;
-            if (d == 0) { p[HD] = mx; p[HD + 1] = lt; }
+            const uint16_t* vr = a.vcache + ((size_t)(pg[tl / kPageTokens] * a.hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD;
+            const u4_t vw = *reinterpret_cast<const u4_t*>(vr + ch * 8);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = dword_at(vw, i);
+                v[2 * i] = kv_decode<F16>(w & 0xffffu);
+                v[2 * i + 1] = kv_decode<F16>(w >> 16);
+            }
         }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float p = sc[g][tl];
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[g][i] = fmaf(p, v[i], o[g][i]);
+        }
+    }
+    const bool direct = a.n_splits == 1;
+    float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) red[sl][ch * 8 + i] = o[g][i];
+        __syncthreads();
+        if (tid < HD) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < NS; j++) acc += red[j][tid];
+            if (direct) a.out[(size_t)(kvh * G + g) * HD + tid] = acc / stat[1][g];
+            else st_agent(rec + g * HD + tid, acc);
+        }
+        __syncthreads();
     }
     if (direct) return;
-    fence_release();   // every wave's partial stores complete before the arrival
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(a.counters + kvh, 1u);
-        is_last = (old == (uint32_t)a.n_splits - 1);
+    if (tid < G) {
+        st_agent(rec + G * HD + tid, n > 0 ? stat[0][tid] : -INFINITY);
+        st_agent(rec + G * HD + G + tid, n > 0 ? stat[1][tid] : 0.f);
     }
-    __syncthreads();
-    if (!is_last) return;
-    fence_acquire();
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD, d = idx % HD, qh = kvh * G + g;
-        const float* p = a.part + (size_t)qh * a.n_splits * (HD + 2);
+    if (!arrive_last(a.counters + kvh, a.n_splits)) return;
+
+    // -- merge the splits of this KV head (log-sum-exp in base 2)
+    const float* base = a.part + (size_t)kvh * a.n_splits * REC;
+    if (tid < G) {
         float mx = -INFINITY;
-        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, __builtin_nontemporal_load(p + sp * (HD + 2) + HD));
-        float lt = 0.f, ot = 0.f;
+        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, ld_agent(base + (size_t)sp * REC + G * HD + tid));
+        float lt = 0.f;
         for (int sp = 0; sp < a.n_splits; sp++) {
-            const float ms = __builtin_nontemporal_load(p + sp * (HD + 2) + HD);
-            const float c = ms == -INFINITY ? 0.f : exp2f(ms - mx);
-            lt += __builtin_nontemporal_load(p + sp * (HD + 2) + HD + 1) * c;
-            ot += __builtin_nontemporal_load(p + sp * (HD + 2) + d) * c;
+            const float ms = ld_agent(base + (size_t)sp * REC + G * HD + tid);
+            if (ms != -INFINITY) lt += ld_agent(base + (size_t)sp * REC + G * HD + G + tid) * exp2f(ms - mx);
         }
-        a.out[qh * HD + d] = ot / lt;
+        stat[0][tid] = mx;
+        stat[1][tid] = lt;
     }
-    if (tid == 0) a.counters[kvh] = 0u;
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD;
+        const float mx = stat[0][g];
+        float acc = 0.f;
+        for (int sp = 0; sp < a.n_splits; sp++) {
+            const float ms = ld_agent(base + (size_t)sp * REC + G * HD + g);
+            if (ms != -INFINITY) acc += ld_agent(base + (size_t)sp * REC + idx) * exp2f(ms - mx);
+        }
+        a.out[(size_t)kvh * G * HD + idx] = acc / stat[1][g];
+    }
 }
 
 // Standalone greedy argmax (model_ops.rs:203-260) used by tests.
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* logits, uint32_t n, uint64_t* partial,
                                                           uint32_t* counter, uint32_t* out) {
     __shared__ uint64_t wbest[kWaves];
-    __shared__ int is_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t b = 0ull;
     for (uint32_t i = blockIdx.x * kThreads + tid; i < n; i += gridDim.x * kThreads) b = max(b, argmax_key(logits[i], i));
@@ -725,15 +748,11 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* logits, u
     __syncthreads();
     if (tid == 0) {
         for (int i = 1; i < kWaves; i++) wbest[0] = max(wbest[0], wbest[i]);
-        partial[blockIdx.x] = wbest[0];
-        fence_release();
-        is_last = atomicAdd(counter, 1u) == gridDim.x - 1;
+        st_agent(partial + blockIdx.x, wbest[0]);
     }
-    __syncthreads();
-    if (!is_last) return;
-    fence_acquire();
+    if (!arrive_last(counter, gridDim.x)) return;
     b = 0ull;
-    for (int i = tid; i < (int)gridDim.x; i += kThreads) b = max(b, __builtin_nontemporal_load(partial + i));
+    for (int i = tid; i < (int)gridDim.x; i += kThreads) b = max(b, ld_agent(partial + i));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
     __syncthreads();
@@ -742,7 +761,6 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* logits, u
     if (tid == 0) {
         for (int i = 1; i < kWaves; i++) wbest[0] = max(wbest[0], wbest[i]);
         *out = wbest[0] ? 0xffffffffu - (uint32_t)(wbest[0] & 0xffffffffu) : 0u;
-        *counter = 0u;
     }
 }
 
@@ -763,27 +781,55 @@ hipError_t attention_dispatch(const AttnArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int MODE>
+hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
+    const size_t lds = matvec_lds_bytes(a.k);
+    const uint32_t ta = a.type_a, tb = a.nseg > 2 ? a.type_b : a.type_a;
+#define RIBN_MV(A, B)                                                             \
+    if (ta == A && tb == B) {                                                     \
+        matvec_kernel<A, B, MODE><<<n_wg, kThreads, lds, st>>>(a);                \
+        return hipGetLastError();                                                 \
+    }
+    if constexpr (MODE == MV_STORE) {
+        RIBN_MV(12, 14) RIBN_MV(14, 12) RIBN_MV(12, 8) RIBN_MV(8, 12) RIBN_MV(14, 8) RIBN_MV(8, 14)
+    }
+    RIBN_MV(12, 12) RIBN_MV(14, 14) RIBN_MV(8, 8)
+#undef RIBN_MV
+    return hipErrorInvalidValue;
+}
+
 }  // namespace
 
-size_t matvec_lds_bytes(int k) { return (size_t)k * 2 + (size_t)(k / 16) * 4 + kTailBytes; }
+size_t matvec_lds_bytes(int k) {
+    size_t b = mv_red_offset(k) + 64 * 4;
+    if (k <= kStageF32) b += (size_t)k * 4;
+    return b;
+}
 
 int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * kWaves * (a.mode == MV_SILU ? 1 : 2); }
 
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
-    if (n_wg <= 0) return hipErrorInvalidValue;
-    matvec_kernel<<<n_wg, kThreads, matvec_lds_bytes(a.k), st>>>(a);
-    return hipGetLastError();
+    if (n_wg <= 0 || a.k <= 0 || a.k % 16) return hipErrorInvalidValue;
+    switch (a.mode) {
+    case MV_STORE: return matvec_dispatch<MV_STORE>(a, n_wg, st);
+    case MV_ADD: return matvec_dispatch<MV_ADD>(a, n_wg, st);
+    case MV_SILU: return matvec_dispatch<MV_SILU>(a, n_wg, st);
+    case MV_HEAD: return matvec_dispatch<MV_HEAD>(a, n_wg, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
-    if (a.n_splits < 1 || a.n_splits > kMaxSplits || a.hq % a.hkv) return hipErrorInvalidValue;
+    if (a.n_splits < 1 || a.n_splits > kMaxSplits || a.hkv < 1 || a.hq % a.hkv || a.rot > a.hd || a.rot % 2)
+        return hipErrorInvalidValue;
     if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
     if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_embed(const QMat& w, int hidden, float* h, const StepCtl* ctl, hipStream_t st) {
-    embed_kernel<<<(hidden + kThreads - 1) / kThreads, kThreads, 0, st>>>(w, hidden, h, ctl);
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t st) {
+    if (a.half_rot > kThreads) return hipErrorInvalidValue;
+    embed_kernel<<<(a.hidden + kThreads - 1) / kThreads, kThreads, 0, st>>>(a);
     return hipGetLastError();
 }
 

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <map>
 #include <memory>
 #include <string>
@@ -49,8 +50,11 @@ struct Submission {
     hipEvent_t done = nullptr;
 };
 
+// Decode-attention splits: about 64 positions per workgroup, a power of two
+// (one graph per bucket), at most kMaxSplits; a split then covers at most
+// kMaxSplitTokens positions for every context the loader admits.
 int splits_for_ctx(int ctx) {
-    int want = (ctx + 31) / 32;
+    const int want = (ctx + 63) / 64;
     int s = 1;
     while (s < want && s < kMaxSplits) s <<= 1;
     return s;
@@ -84,7 +88,8 @@ struct ribn_rocm_model {
     // activations / scratch
     float *h = nullptr, *raw = nullptr, *qbuf = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
     float* part = nullptr;
-    uint32_t* counters = nullptr;   // [hq + hkv] qkv, [hkv] attention, [1] head
+    uint32_t* counters = nullptr;   // [hkv] attention, [1] head
+    float *inv_freq = nullptr, *rope = nullptr;
     uint64_t* head_partial = nullptr;
     int head_wgs = 0;
 
@@ -268,78 +273,95 @@ void build_launches(ribn_rocm_model* M) {
     M->wg_qkv.clear(); M->wg_o.clear(); M->wg_gu.clear(); M->wg_down.clear();
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
-        MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_QKV, M->d_ctl);
-        q.items_per_wave = 1;   // 8 rows per workgroup: divides every head_dim
+        MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
+        q.items_per_wave = 2;
         q.nseg = 3;
-        q.seg[0].w = y.q; q.seg[0].out = M->raw; q.seg[0].bias = y.q_bias; q.seg[0].kind = 0;
-        q.seg[1].w = y.k; q.seg[1].out = M->raw + qd; q.seg[1].bias = y.k_bias; q.seg[1].kind = 1;
-        q.seg[2].w = y.v; q.seg[2].out = M->raw + qd + kd; q.seg[2].bias = y.v_bias; q.seg[2].kind = 2;
-        q.qkv.raw = M->raw;
-        q.qkv.q_out = M->qbuf;
-        q.qkv.kcache = y.kc;
-        q.qkv.vcache = y.vc;
-        q.qkv.q_norm = y.q_norm;
-        q.qkv.k_norm = y.k_norm;
-        q.qkv.counters = M->counters;
-        q.qkv.hq = M->hq; q.qkv.hkv = M->hkv; q.qkv.hd = M->hd; q.qkv.rot = M->rot;
-        q.qkv.rope_base = M->base; q.qkv.eps = M->eps;
-        q.qkv.kv_f16 = M->kv_f16 ? 1 : 0;
+        q.type_a = y.q.type;
+        q.type_b = y.v.type;
+        q.seg[0].w = y.q; q.seg[0].out = M->raw; q.seg[0].bias = y.q_bias;
+        q.seg[1].w = y.k; q.seg[1].out = M->raw + qd; q.seg[1].bias = y.k_bias;
+        q.seg[2].w = y.v; q.seg[2].out = M->raw + qd + kd; q.seg[2].bias = y.v_bias;
         M->wg_qkv.push_back(layout_segments(q));
         M->mv_qkv.push_back(q);
 
         MvArgs o = mv_base(M->attn, nullptr, 0.f, qd, MV_ADD, M->d_ctl);
         o.nseg = 1;
         o.seg[0].w = y.o; o.seg[0].out = M->h;
-        o.items_per_wave = choose_ipw(M->H / 2, 4);
+        o.type_a = o.type_b = y.o.type;
+        o.items_per_wave = 2;
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
 
         MvArgs g = mv_base(M->h, y.ffn_norm, M->eps, M->H, MV_SILU, M->d_ctl);
         g.nseg = 1;
         g.seg[0].w = y.gate; g.seg[0].w2 = y.up; g.seg[0].out = M->act;
-        g.items_per_wave = choose_ipw(M->F, 4);
+        g.type_a = g.type_b = y.gate.type;
+        g.items_per_wave = 4;
         M->wg_gu.push_back(layout_segments(g));
         M->mv_gu.push_back(g);
 
         MvArgs d = mv_base(M->act, nullptr, 0.f, M->F, MV_ADD, M->d_ctl);
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
-        d.items_per_wave = choose_ipw(M->H / 2, 4);
+        d.type_a = d.type_b = y.down.type;
+        d.items_per_wave = 2;
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
     MvArgs hdv = mv_base(M->h, M->out_norm, M->eps, M->H, MV_HEAD, M->d_ctl);
     hdv.nseg = 1;
     hdv.seg[0].w = M->out; hdv.seg[0].out = M->logits;
+    hdv.type_a = hdv.type_b = M->out.type;
     hdv.items_per_wave = choose_ipw(M->V / 2, 8);
     hdv.head.partial = M->head_partial;
-    hdv.head.counter = M->counters + M->hq + 2 * M->hkv;
+    hdv.head.counter = M->counters + M->hkv;
     M->head_wgs = layout_segments(hdv);
     M->mv_head = hdv;
 }
 
+AttnArgs attn_args(ribn_rocm_model* M, int l, int n_splits) {
+    AttnArgs at{};
+    const Layer& y = M->layers[l];
+    at.raw = M->raw;
+    at.q_norm = y.q_norm;
+    at.k_norm = y.k_norm;
+    at.rope = M->rope;
+    at.kcache = y.kc;
+    at.vcache = y.vc;
+    at.part = M->part;
+    at.counters = M->counters;
+    at.out = M->attn;
+    at.ctl = M->d_ctl;
+    at.hq = M->hq; at.hkv = M->hkv; at.hd = M->hd; at.rot = M->rot;
+    at.n_splits = n_splits;
+    at.kv_f16 = M->kv_f16 ? 1 : 0;
+    at.eps = M->eps;
+    at.scale_log2 = 1.4426950408889634f / std::sqrt((float)M->hd);
+    return at;
+}
+
 // One step of the token loop for the active sequence (decode.rs:550-640):
-// embedding -> L x [QKV(+norm,+rope,+KV append) -> attention -> O(+residual)
-// -> gate/up(+norm,+SwiGLU) -> down(+residual)] -> head(+norm,+argmax) or advance.
+// embedding (+rope table) -> L x [QKV(+norm) -> attention(+q/k norm, rope, KV
+// append) -> O(+residual) -> gate/up(+norm,+SwiGLU) -> down(+residual)]
+// -> head(+norm,+argmax) or advance.
 hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trace) {
     hipStream_t st = M->stream;
-    hipError_t e = launch_embed(M->embd, M->H, M->h, M->d_ctl, st);
+    EmbedArgs ea{};
+    ea.w = M->embd;
+    ea.hidden = M->H;
+    ea.h = M->h;
+    ea.ctl = M->d_ctl;
+    ea.inv_freq = M->inv_freq;
+    ea.rope = M->rope;
+    ea.half_rot = M->rot / 2;
+    hipError_t e = launch_embed(ea, st);
     if (e != hipSuccess) return e;
     if (trace && (e = hipMemcpyAsync(trace, M->h, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
         return e;
-    AttnArgs at{};
-    at.q = M->qbuf;
-    at.part = M->part;
-    at.counters = M->counters + M->hq + M->hkv;
-    at.out = M->attn;
-    at.ctl = M->d_ctl;
-    at.hq = M->hq; at.hkv = M->hkv; at.hd = M->hd; at.n_splits = n_splits;
-    at.scale_log2 = 1.4426950408889634f / std::sqrt((float)M->hd);
-    at.kv_f16 = M->kv_f16 ? 1 : 0;
+    AttnArgs at = attn_args(M, 0, n_splits);
     for (int l = 0; l < M->L; l++) {
         if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
-        at.kcache = M->layers[l].kc;
-        at.vcache = M->layers[l].vc;
+        at = attn_args(M, l, n_splits);
         if ((e = launch_attention(at, st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_o[l], M->wg_o[l], st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st)) != hipSuccess) return e;
@@ -353,8 +375,20 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
     return launch_advance(M->d_ctl, st);
 }
 
+// RIBN_ROCM_EAGER=1 launches the chain directly instead of replaying graphs
+// (same kernels and arguments). Used for profiler runs: rocprofv3's kernel
+// tracer crashes the host process inside HIP graph capture on this image.
+bool eager_mode() {
+    static const bool eager = [] {
+        const char* v = std::getenv("RIBN_ROCM_EAGER");
+        return v && v[0] == '1';
+    }();
+    return eager;
+}
+
 hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
     const int ns = splits_for_ctx(ctx);
+    if (eager_mode()) return enqueue_step(M, head, ns, nullptr);
     const int key = ns * 2 + (head ? 1 : 0);
     auto it = M->graphs.find(key);
     if (it == M->graphs.end()) {
@@ -493,6 +527,10 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     M->context = o.context_tokens ? o.context_tokens : (uint32_t)std::min<uint64_t>(ctx_meta ? ctx_meta : 4096, 4096);
     M->max_seqs = o.max_sequences ? o.max_sequences : 8;
     M->max_batch_tokens = o.max_batch_tokens ? o.max_batch_tokens : 2048;
+    if (M->context > (uint32_t)(kMaxSplits * kMaxSplitTokens)) {
+        set_err(err, err_len, "context_tokens above " + std::to_string(kMaxSplits * kMaxSplitTokens));
+        return RIBN_ERR_INVALID;
+    }
     M->max_pages = (int)((M->context + kPageTokens - 1) / kPageTokens);
     M->kv_pages = o.kv_pages ? o.kv_pages : (uint32_t)(M->max_seqs * M->max_pages);
     if ((int)M->kv_pages < M->max_pages) M->kv_pages = M->max_pages;
@@ -543,6 +581,9 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             if ((msg = validate_type(t, nm.c_str(), true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
             if ((rc = upload_mat(t, m.rows, m.k, m.q)) != RIBN_OK) return rc;
         }
+        if (y.q.type != y.k.type) {
+            set_err(err, err_len, "attn_q and attn_k must share a value type"); return RIBN_ERR_FORMAT;
+        }
         if (y.gate.type != y.up.type) {
             set_err(err, err_len, "ffn_gate and ffn_up must share a value type"); return RIBN_ERR_FORMAT;
         }
@@ -576,8 +617,15 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(dalloc(M, &M->attn, sizeof(float) * qd));
     HIPCHK(dalloc(M, &M->act, sizeof(float) * M->F));
     HIPCHK(dalloc(M, &M->logits, sizeof(float) * M->V));
-    HIPCHK(dalloc(M, &M->part, sizeof(float) * (size_t)qd / M->hd * kMaxSplits * (M->hd + 2)));
-    const int n_counters = M->hq + 2 * M->hkv + 1;
+    HIPCHK(dalloc(M, &M->part, sizeof(float) * (size_t)kMaxSplits * (qd + 2 * M->hq)));
+    const int n_counters = M->hkv + 1;
+    {
+        std::vector<float> inv(M->rot / 2);
+        for (int p = 0; p < M->rot / 2; p++) inv[p] = std::pow(M->base, -(2.0f * (float)p) / (float)M->rot);
+        HIPCHK(dalloc(M, &M->inv_freq, sizeof(float) * inv.size()));
+        HIPCHK(dalloc(M, &M->rope, sizeof(float) * M->rot));
+        HIPCHK(hipMemcpy(M->inv_freq, inv.data(), sizeof(float) * inv.size(), hipMemcpyHostToDevice));
+    }
     HIPCHK(dalloc(M, &M->counters, sizeof(uint32_t) * n_counters));
     HIPCHK(hipMemsetAsync(M->counters, 0, sizeof(uint32_t) * n_counters, M->stream));
     HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * ((size_t)M->V / 2 + 64)));
@@ -587,6 +635,8 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(dalloc(M, &M->d_pages, sizeof(int32_t) * (size_t)slots * M->max_pages));
     HIPCHK(dalloc(M, &M->d_tokens, sizeof(uint32_t) * (size_t)slots * (M->context + 1)));
     HIPCHK(dalloc(M, &M->d_ctl, sizeof(StepCtl)));
+    HIPCHK(hipMemsetAsync(M->d_pages, 0, sizeof(int32_t) * (size_t)slots * M->max_pages, M->stream));
+    HIPCHK(hipMemsetAsync(M->d_tokens, 0, sizeof(uint32_t) * (size_t)slots * (M->context + 1), M->stream));
     HIPCHK(halloc(M, &M->h_slot_ptr, sizeof(SeqState*) * slots));
     HIPCHK(halloc(M, &M->h_state, sizeof(SeqState) * slots));
     HIPCHK(halloc(M, &M->h_pages, sizeof(int32_t) * (size_t)slots * M->max_pages));
@@ -1017,6 +1067,7 @@ extern "C" int ribn_rocm_gemv(uint32_t type, const uint8_t* blocks, uint64_t row
     }
     MvArgs a = mv_base(dx, dw, eps, (int)k, MV_STORE, nullptr);
     a.nseg = 1;
+    a.type_a = a.type_b = type;
     a.seg[0].w = q;
     a.seg[0].out = dy;
     a.items_per_wave = choose_ipw((int)(rows / 2), 4);
@@ -1041,6 +1092,7 @@ extern "C" int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, ui
     HIPCHK(hipMemcpy(dx, hx.data(), sizeof(float) * k, hipMemcpyHostToDevice));
     MvArgs a = mv_base(dx, nullptr, 0.f, (int)k, MV_STORE, nullptr);
     a.nseg = 1;
+    a.type_a = a.type_b = type;
     a.seg[0].w = q;
     a.seg[0].out = dy;
     a.items_per_wave = choose_ipw((int)(rows / 2), 4);
@@ -1075,11 +1127,64 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
         type_layout(q.type, &be, &bb);
         return (uint64_t)q.rows * q.nb * bb;
     };
+    bool attn = false;
+    AttnArgs at{};
+    std::vector<int32_t> bench_pages;
+    struct PageReturn {
+        ribn_rocm_model* M;
+        std::vector<int32_t>* p;
+        ~PageReturn() {
+            if (!p->empty()) {
+                hipStreamSynchronize(M->stream);
+                give_pages(M, *p);
+            }
+        }
+    } page_return{M, &bench_pages};
     switch (which) {
     case 0: a = M->mv_gu[0]; nwg = M->wg_gu[0]; *bytes = qbytes(a.seg[0].w) + qbytes(a.seg[0].w2); break;
     case 1: a = M->mv_down[0]; nwg = M->wg_down[0]; a.mode = MV_STORE; a.seg[0].out = M->act; *bytes = qbytes(a.seg[0].w); break;
     case 2: a = M->mv_head; nwg = M->head_wgs; a.mode = MV_STORE; *bytes = qbytes(a.seg[0].w); break;
+    case 3: case 4:
+        a = M->mv_qkv[0]; nwg = M->wg_qkv[0];
+        *bytes = qbytes(a.seg[0].w) + qbytes(a.seg[1].w) + qbytes(a.seg[2].w);
+        break;
+    case 5: a = M->mv_o[0]; nwg = M->wg_o[0]; a.mode = MV_STORE; a.seg[0].out = M->act; *bytes = qbytes(a.seg[0].w); break;
+    case 6: {
+        // decode attention of layer 0 for a scratch sequence holding exactly
+        // `ctx` positions (the current token is position ctx-1)
+        const int ctx = (int)*bytes;
+        if (ctx < 1 || (uint32_t)ctx > M->context)
+            return fail(nullptr, err, err_len, "attention bench context outside the prepared context", RIBN_ERR_INVALID);
+        if (!take_pages(M, (uint32_t)ctx, &bench_pages))
+            return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
+        const int slot = (int)M->max_seqs;
+        const uint32_t tok0 = 0;
+        HIPCHK(reset_slot(M, slot, bench_pages, &tok0, 1));
+        M->h_state[slot].pos = ctx - 1;
+        HIPCHK(hipMemcpyAsync(&M->d_slots[slot], &M->h_state[slot], sizeof(SeqState), hipMemcpyHostToDevice, M->stream));
+        HIPCHK(select_slot(M, slot));
+        attn = true;
+        at = attn_args(M, 0, splits_for_ctx(ctx));
+        *bytes = 0;
+        break;
+    }
     default: return fail(nullptr, err, err_len, "unknown kernel selector", RIBN_ERR_INVALID);
+    }
+    if (attn) {
+        hipEvent_t e0, e1;
+        HIPCHK(hipEventCreate(&e0));
+        HIPCHK(hipEventCreate(&e1));
+        for (int i = 0; i < 3; i++) HIPCHK(launch_attention(at, M->stream));
+        HIPCHK(hipEventRecord(e0, M->stream));
+        for (uint32_t i = 0; i < iters; i++) HIPCHK(launch_attention(at, M->stream));
+        HIPCHK(hipEventRecord(e1, M->stream));
+        HIPCHK(hipEventSynchronize(e1));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+        *avg_ms = ms / iters;
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+        return RIBN_OK;
     }
     hipEvent_t e0, e1;
     HIPCHK(hipEventCreate(&e0));
