@@ -215,7 +215,7 @@ __global__ void advance_kernel(const StepCtl* ctl) {
 // lies in [2^14, 2^15), plus fp32 sums of each 16 staged values. Inputs up to
 // kStageF32 elements are read once (kept as fp32 in LDS between the statistics
 // and the conversion); longer ones are read twice. Returns 2^-e.
-constexpr int kStageF32 = 8192;
+constexpr int kStageF32 = 16384;
 
 // LDS layout of the matvec: [k] fp16 | [k/16] fp32 sums | 64 fp32 reduction
 // slots | (k <= kStageF32) [k] fp32 staging; 16-byte aligned pieces.
@@ -340,14 +340,15 @@ struct Unit<12> {
 template <>
 struct Unit<14> {
     static constexpr int kPerBlock = 8;
-    struct Raw { u4_t ql, qh, sc; uint32_t d; };
+    struct Raw { u4_t ql, qh; int32_t sl, sh; uint32_t d; };
     static __device__ __forceinline__ Raw load(const QMat& w, size_t row, int u) {
         const size_t nb = w.nb, bi = row * nb + (u >> 3);
-        const int c = u & 7;
+        const int c = u & 7, il = ((c >> 2) * 4 + ((c >> 1) & 1)) * 2 + (c & 1);
         Raw r;
         r.ql = ld_nt16(w.a + row * nb * 128 + (size_t)u * 16);
         r.qh = ld_nt16(w.b + bi * 64 + 16 * (2 * (c >> 2) + (c & 1)));
-        r.sc = ld16(w.c + bi * 16);
+        r.sl = *reinterpret_cast<const int8_t*>(w.c + bi * 16 + il);
+        r.sh = *reinterpret_cast<const int8_t*>(w.c + bi * 16 + il + 4);
         r.d = *reinterpret_cast<const uint16_t*>(w.d + bi * 2);
         return r;
     }
@@ -362,9 +363,6 @@ struct Unit<14> {
             lo[i] = (l & m4) | (((h >> sl) & m2) << 4);
             hi[i] = ((l >> 4) & m4) | (((h >> sh) & m2) << 4);
         }
-        const int il = (chunk * 4 + vb) * 2 + hf, ih = il + 4;
-        const float scl = (float)(int8_t)byte_at(dword_at(r.sc, il >> 2), il & 3);
-        const float sch = (float)(int8_t)byte_at(dword_at(r.sc, ih >> 2), ih & 3);
         const float d = h2f(r.d);
         const int xo = blk * 256 + chunk * 128 + vb * 32 + 16 * hf;
         const u4_t xa = xs4[xo / 8], xb = xs4[xo / 8 + 1];
@@ -372,8 +370,8 @@ struct Unit<14> {
         const float X0 = gs[xo / 16], X1 = gs[xo / 16 + 4];
         const float s0 = dot16(lo[0], lo[1], lo[2], lo[3], xa, xb);
         const float s1 = dot16(hi[0], hi[1], hi[2], hi[3], ya, yb);
-        acc = fmaf(d * scl, fmaf(-1056.f, X0, s0), acc);
-        acc = fmaf(d * sch, fmaf(-1056.f, X1, s1), acc);
+        acc = fmaf(d * (float)r.sl, fmaf(-1056.f, X0, s0), acc);
+        acc = fmaf(d * (float)r.sh, fmaf(-1056.f, X1, s1), acc);
         return acc;
     }
 };
@@ -397,35 +395,94 @@ struct Unit<8> {
     }
 };
 
-// Two rows (A, B) at once; lanes stride over units, two units in flight per row.
+// A load group: two units of each of the two rows of an item, per lane.
 template <int T>
-__device__ __forceinline__ void rows2(const QMat& wa, size_t ra, const QMat& wb, size_t rb, const u4_t* xs4,
-                                      const float* gs, float& acc_a, float& acc_b) {
+struct Group {
+    typename Unit<T>::Raw a0, b0, a1, b1;
+};
+
+// Where a wave's work lives: items (two rows each, or one gate/up pair) of one
+// segment, walked as a flat sequence of load groups so that the next group's
+// 128-bit loads are always in flight while the current group is computed.
+struct WaveWork {
+    const QMat* wa;
+    const QMat* wb;        // second row's matrix (the up matrix for gate/up pairs)
+    int first_item, n_items, n_rows, ngr, n_units;
+    bool pair;
+};
+
+template <int T>
+__device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int q) {
     using U = Unit<T>;
-    const int n_units = (int)wa.nb * U::kPerBlock;
+    const int it = q / w.ngr, gi = q % w.ngr;
+    const int item = w.first_item + it * kWaves;
+    const int ra = w.pair ? item : 2 * item;
+    const int rb = w.pair ? item : min(ra + 1, w.n_rows - 1);
     const int lane = threadIdx.x & 63;
-    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-    int u = lane;
-    for (; u + 64 < n_units; u += 128) {
-        auto pa0 = U::load(wa, ra, u), pb0 = U::load(wb, rb, u);
-        auto pa1 = U::load(wa, ra, u + 64), pb1 = U::load(wb, rb, u + 64);
-        a0 = U::apply(pa0, u, xs4, gs, a0);
-        b0 = U::apply(pb0, u, xs4, gs, b0);
-        a1 = U::apply(pa1, u + 64, xs4, gs, a1);
-        b1 = U::apply(pb1, u + 64, xs4, gs, b1);
+    int u0 = gi * 128 + lane, u1 = u0 + 64;
+    u0 = u0 < w.n_units ? u0 : 0;
+    u1 = u1 < w.n_units ? u1 : 0;
+    g.a0 = U::load(*w.wa, (size_t)ra, u0);
+    g.b0 = U::load(*w.wb, (size_t)rb, u0);
+    g.a1 = U::load(*w.wa, (size_t)ra, u1);
+    g.b1 = U::load(*w.wb, (size_t)rb, u1);
+}
+
+template <int T, int MODE>
+__device__ __forceinline__ void mv_body(const MvArgs& a, const MvSeg& sg, const WaveWork& w, Group<T>& cur,
+                                        const u4_t* xs4, const float* gs, float oscale, uint64_t& best) {
+    using U = Unit<T>;
+    const int lane = threadIdx.x & 63;
+    const int total = w.n_items * w.ngr;
+    float a0 = 0.f, b0 = 0.f;
+    for (int q = 0; q < total; q++) {
+        Group<T> nxt;
+        if (q + 1 < total) load_group<T>(nxt, w, q + 1);
+        const int gi = q % w.ngr;
+        const int u0 = gi * 128 + lane, u1 = u0 + 64;
+        if (u0 < w.n_units) {
+            a0 = U::apply(cur.a0, u0, xs4, gs, a0);
+            b0 = U::apply(cur.b0, u0, xs4, gs, b0);
+        }
+        if (u1 < w.n_units) {
+            a0 = U::apply(cur.a1, u1, xs4, gs, a0);
+            b0 = U::apply(cur.b1, u1, xs4, gs, b0);
+        }
+        if (gi == w.ngr - 1) {
+            float ya = wave_sum(a0) * oscale, yb = wave_sum(b0) * oscale;
+            a0 = b0 = 0.f;
+            const int item = w.first_item + (q / w.ngr) * kWaves;
+            const int ra = w.pair ? item : 2 * item;
+            const int rb = w.pair ? item : ra + 1;
+            if (lane == 0) {
+                const bool has_b = !w.pair && rb < w.n_rows;
+                if (sg.bias) {
+                    ya += sg.bias[ra];
+                    if (has_b) yb += sg.bias[rb];
+                }
+                if constexpr (MODE == MV_ADD) {
+                    sg.out[ra] += ya;
+                    if (has_b) sg.out[rb] += yb;
+                } else if constexpr (MODE == MV_SILU) {
+                    sg.out[ra] = ya / (1.0f + expf(-ya)) * yb;
+                } else {
+                    sg.out[ra] = ya;
+                    if (has_b) sg.out[rb] = yb;
+                    if constexpr (MODE == MV_HEAD) {
+                        best = max(best, argmax_key(ya, (uint32_t)ra));
+                        if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
+                    }
+                }
+            }
+        }
+        if (q + 1 < total) cur = nxt;
     }
-    if (u < n_units) {
-        auto pa = U::load(wa, ra, u), pb = U::load(wb, rb, u);
-        a0 = U::apply(pa, u, xs4, gs, a0);
-        b0 = U::apply(pb, u, xs4, gs, b0);
-    }
-    acc_a = wave_sum(a0 + a1);
-    acc_b = wave_sum(b0 + b1);
 }
 
 // Fused dequant-matvec (gguf_gemv qwen_reference.rs:31-40; q*_gemv_warp
 // kernels/quantized/q4_k.cu:103, q6_k.cu:45, q8_0.cu:27). Each wave computes
-// two rows per item (or a gate/up pair); rows of a workgroup are contiguous.
+// two rows per item (or a gate/up pair); the first weight loads are issued
+// before the input is staged, so HBM streaming overlaps the prologue.
 template <int TA, int TB, int MODE>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -433,7 +490,6 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
     float* red = reinterpret_cast<float*>(lds + mv_red_offset(a.k));
     float* xf = red + 64;
-    const float oscale = stage_x(a, xs, gs, xf, red);
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
 
     const int wg = blockIdx.x;
@@ -443,42 +499,31 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     const MvSeg& sg = a.seg[si];
     const int lwg = wg - sg.wg_begin;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int ipw = a.items_per_wave;
     constexpr bool pair = MODE == MV_SILU;
-    constexpr int rows_per_item = pair ? 1 : 2;
-    const int n_rows = (int)sg.w.rows;
+    WaveWork w;
+    w.wa = &sg.w;
+    w.wb = pair ? &sg.w2 : &sg.w;
+    w.pair = pair;
+    w.n_rows = (int)sg.w.rows;
+    w.first_item = lwg * a.items_per_wave * kWaves + wave;
+    const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
+    w.n_items = max(0, min(a.items_per_wave, (n_item_total - w.first_item + kWaves - 1) / kWaves));
     uint64_t best = 0ull;
-
-    for (int it = 0; it < ipw; it++) {
-        const int item = (lwg * ipw + it) * kWaves + wave;
-        const int ra = item * rows_per_item;
-        if (ra >= n_rows) break;
-        const int rb = pair ? ra : min(ra + 1, n_rows - 1);
-        float ya, yb;
-        if (si == 2 && TB != TA) rows2<TB>(sg.w, (size_t)ra, sg.w, (size_t)rb, xs4, gs, ya, yb);
-        else rows2<TA>(sg.w, (size_t)ra, pair ? sg.w2 : sg.w, (size_t)rb, xs4, gs, ya, yb);
-        ya *= oscale;
-        yb *= oscale;
-        if (lane == 0) {
-            const bool has_b = !pair && ra + 1 < n_rows;
-            if (sg.bias) {
-                ya += sg.bias[ra];
-                if (has_b) yb += sg.bias[rb];
-            }
-            if constexpr (MODE == MV_ADD) {
-                sg.out[ra] += ya;
-                if (has_b) sg.out[rb] += yb;
-            } else if constexpr (MODE == MV_SILU) {
-                sg.out[ra] = ya / (1.0f + expf(-ya)) * yb;
-            } else {
-                sg.out[ra] = ya;
-                if (has_b) sg.out[rb] = yb;
-                if constexpr (MODE == MV_HEAD) {
-                    best = max(best, argmax_key(ya, (uint32_t)ra));
-                    if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
-                }
-            }
-        }
+    const bool second = si == 2 && TB != TA;
+    if (!second) {
+        w.n_units = (int)sg.w.nb * Unit<TA>::kPerBlock;
+        w.ngr = (w.n_units + 127) / 128;
+        Group<TA> g;
+        if (w.n_items > 0) load_group<TA>(g, w, 0);
+        const float oscale = stage_x(a, xs, gs, xf, red);
+        mv_body<TA, MODE>(a, sg, w, g, xs4, gs, oscale, best);
+    } else {
+        w.n_units = (int)sg.w.nb * Unit<TB>::kPerBlock;
+        w.ngr = (w.n_units + 127) / 128;
+        Group<TB> g;
+        if (w.n_items > 0) load_group<TB>(g, w, 0);
+        const float oscale = stage_x(a, xs, gs, xf, red);
+        mv_body<TB, MODE>(a, sg, w, g, xs4, gs, oscale, best);
     }
 
     if constexpr (MODE == MV_HEAD) {
@@ -518,24 +563,57 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
 // (attn_score_gqa_paged, model_ops.rs:442-590; host equations
 // qwen_reference.rs:368-461, dense Qwen3: no gate). Workgroup (split, kv head);
 // the G = hq/hkv query heads of a KV head share every K/V load.
-//  prologue: q (G heads) and k of the current token get per-head RMSNorm
-//            (qwen_reference.rs:382-400) and NeoX rope from the step table; the
-//            workgroup whose split holds the current position appends k, v to
-//            the cache (kv_append_f16, model_ops.rs:1258);
-//  phase 1:  one token per lane, full-row q.k for the G heads -> LDS;
-//  phase 2:  exact softmax statistics of the split (max, sum of exp2);
-//  phase 3:  P.V with 16-byte V loads, lanes over (dims, token slices);
-//  merge:    splits are combined by log-sum-exp in the last workgroup.
-// Every key and value, including the current token's, is read back at the
-// cache's precision, as the reference reads its F16 cache.
+//  * the split's K and V are staged in LDS in tiles of 64 positions (16-byte
+//    loads, the first tile issued before the prologue so its latency overlaps);
+//  * prologue: q (G heads) and k of the current token get per-head RMSNorm
+//    (qwen_reference.rs:382-400) and NeoX rope from the step table; the
+//    workgroup whose split holds the current position appends k, v
+//    (kv_append_f16, model_ops.rs:1258);
+//  * scores: 4 lanes per position, 1/4 of head_dim each, for all G heads;
+//  * exact softmax statistics of the split, then P.V over the V tiles;
+//  * splits are merged by log-sum-exp in the last workgroup of a KV head.
+// Every key and value, including the current token's, is used at the cache's
+// precision, as the reference reads its F16 cache.
+constexpr int kTile = 64;
+
+template <int HD, bool F16>
+struct KvTile {
+    static constexpr int kLoads = kTile * HD * 2 / 16 / kThreads;   // 16-byte loads per thread
+    u4_t r[kLoads];
+    // position i*kThreads/(HD/8)... : load index j -> (token, chunk)
+    __device__ __forceinline__ void load(const uint16_t* cache, const int* pg, int hkv, int kvh, int c0, int n,
+                                         int t0) {
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            const int idx = j * kThreads + threadIdx.x;
+            const int tl = c0 + idx / (HD / 8), ch = idx % (HD / 8);
+            if (tl < n) {
+                const int t = t0 + tl;
+                r[j] = *reinterpret_cast<const u4_t*>(
+                    cache + ((size_t)(pg[tl / kPageTokens] * hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD + ch * 8);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t (*tile)[HD]) const {
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            const int idx = j * kThreads + threadIdx.x;
+            *reinterpret_cast<u4_t*>(&tile[idx / (HD / 8)][(idx % (HD / 8)) * 8]) = r[j];
+        }
+    }
+};
+
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     constexpr int CH = HD / 8;                 // 16-byte chunks per row
-    constexpr int NS = kThreads / CH;          // token slices in phase 3
+    constexpr int NS = kThreads / CH;          // token slices in P.V
     constexpr int REC = G * HD + 2 * G;        // partial record floats
-    __shared__ float buf[G + 2][HD];           // q heads, k, v of the current token
+    constexpr int DQ = HD / 4;                 // dims per lane in the scores
+    __shared__ __attribute__((aligned(16))) float buf[G + 2][HD];   // q heads, k, v of the current token
+    __shared__ __attribute__((aligned(16))) uint16_t kt[kTile][HD];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kTile][HD];
     __shared__ float sc[G][kMaxSplitTokens];   // scores, then probabilities
-    __shared__ float red[NS][HD];              // phase-3 reduction
+    __shared__ float red[NS][HD];              // P.V reduction
     __shared__ float stat[2][G];               // per-head max, sum
     __shared__ int pg[kMaxSplitTokens / kPageTokens];
     const int split = blockIdx.x, kvh = blockIdx.y;
@@ -553,18 +631,22 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     }
     const int t0 = split * per, t1 = min(ctx, t0 + per), n = max(0, t1 - t0);
     const int qd = a.hq * HD, kd = a.hkv * HD;
+    const bool owner = t0 <= pos && pos < t1;
 
-    // -- prologue: raw q/k/v -> LDS, per-head norm, rope
+    for (int i = tid; i < n; i += kThreads)
+        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = s->pages[(t0 + i) / kPageTokens];
     for (int i = tid; i < (G + 2) * HD; i += kThreads) {
         const int r = i / HD, d = i % HD;
         const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
                                  : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
         buf[r][d] = src[d];
     }
-    for (int i = tid; i < n; i += kThreads) {
-        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = s->pages[(t0 + i) / kPageTokens];
-    }
     __syncthreads();
+    KvTile<HD, F16> kpre, vpre;   // first tile in flight during the prologue
+    kpre.load(a.kcache, pg, a.hkv, kvh, 0, n, t0);
+    vpre.load(a.vcache, pg, a.hkv, kvh, 0, n, t0);
+
+    // -- prologue: per-head norm, rope, current token at cache precision
     if (a.q_norm) {
         for (int r = wave; r <= G; r += kWaves) {
             const float* nw = r < G ? a.q_norm : a.k_norm;
@@ -585,62 +667,64 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
         buf[r][p + half] = x0 * sn + x1 * c;
     }
     __syncthreads();
-    const bool owner = t0 <= pos && pos < t1;
+    uint16_t cur_e = 0;
     if (tid < 2 * HD) {
-        // the current token at cache precision (and appended by the owner)
         const int r = G + tid / HD, d = tid % HD;
-        const uint16_t e = kv_encode(buf[r][d], F16 ? 1 : 0);
+        cur_e = kv_encode(buf[r][d], F16 ? 1 : 0);
         if (owner) {
             const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
             uint16_t* dst = (r == G ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
-            dst[d] = e;
+            dst[d] = cur_e;
         }
-        buf[r][d] = kv_decode<F16>(e);
     }
+    // scale q into the log2 domain
+    for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
     __syncthreads();
 
-    // -- phase 1: scores (log2 domain)
-    for (int tl = tid; tl < n; tl += kThreads) {
-        const int t = t0 + tl;
+    // -- scores, tile by tile: lane group of 4 per position
+    const int stl = tid >> 2, part = tid & 3;
+    for (int c0 = 0; c0 < n; c0 += kTile) {
+        if (c0 == 0) kpre.store(kt);
+        else {
+            KvTile<HD, F16> kk;
+            kk.load(a.kcache, pg, a.hkv, kvh, c0, n, t0);
+            kk.store(kt);
+        }
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile && tid < HD) kt[pos - t0 - c0][tid] = cur_e;
+        __syncthreads();
+        const int tl = c0 + stl;
         float acc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0.f;
-        if (t == pos) {
-            for (int d = 0; d < HD; d++) {
-                const float kv = buf[G][d];
 #pragma unroll
-                for (int g = 0; g < G; g++) acc[g] = fmaf(buf[g][d], kv, acc[g]);
-            }
-        } else {
-            const uint16_t* kr = a.kcache + ((size_t)(pg[tl / kPageTokens] * a.hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD;
-#pragma unroll 1
-            for (int c0 = 0; c0 < CH; c0 += 4) {
-                u4_t kw[4];
+        for (int c = 0; c < DQ / 8; c++) {
+            const int d0 = part * DQ + c * 8;
+            const u4_t kw = *reinterpret_cast<const u4_t*>(&kt[stl][d0]);
 #pragma unroll
-                for (int c = 0; c < 4; c++) kw[c] = *reinterpret_cast<const u4_t*>(kr + (c0 + c) * 8);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = dword_at(kw, i);
+                const float k0 = kv_decode<F16>(w & 0xffffu), k1 = kv_decode<F16>(w >> 16);
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t w = dword_at(kw[c], i);
-                        const float k0 = kv_decode<F16>(w & 0xffffu), k1 = kv_decode<F16>(w >> 16);
-                        const int d = (c0 + c) * 8 + 2 * i;
-#pragma unroll
-                        for (int g = 0; g < G; g++) {
-                            const float2 qq = *reinterpret_cast<const float2*>(&buf[g][d]);
-                            acc[g] = fmaf(qq.x, k0, acc[g]);
-                            acc[g] = fmaf(qq.y, k1, acc[g]);
-                        }
-                    }
+                for (int g = 0; g < G; g++) {
+                    const float2 qq = *reinterpret_cast<const float2*>(&buf[g][d0 + 2 * i]);
+                    acc[g] = fmaf(qq.x, k0, acc[g]);
+                    acc[g] = fmaf(qq.y, k1, acc[g]);
                 }
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; g++) sc[g][tl] = acc[g] * a.scale_log2;
+        for (int g = 0; g < G; g++) {
+            acc[g] += __shfl_xor(acc[g], 1);
+            acc[g] += __shfl_xor(acc[g], 2);
+        }
+        if (part == 0 && tl < n) {
+#pragma unroll
+            for (int g = 0; g < G; g++) sc[g][tl] = acc[g];
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
-    // -- phase 2: softmax statistics per head
+    // -- softmax statistics per head
     for (int g = wave; g < G; g += kWaves) {
         float m = -INFINITY;
         for (int tl = lane; tl < n; tl += 64) m = fmaxf(m, sc[g][tl]);
@@ -656,34 +740,40 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // -- phase 3: o[g] = sum_t p[g][t] v[t]
+    // -- o[g] = sum_t p[g][t] v[t]
     const int ch = tid % CH, sl = tid / CH;
     float o[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) o[g][i] = 0.f;
-    for (int tl = sl; tl < n; tl += NS) {
-        const int t = t0 + tl;
-        float v[8];
-        if (t == pos) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = buf[G + 1][ch * 8 + i];
-        } else {
-            const uint16_t* vr = a.vcache + ((size_t)(pg[tl / kPageTokens] * a.hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD;
-            const u4_t vw = *reinterpret_cast<const u4_t*>(vr + ch * 8);
+    for (int c0 = 0; c0 < n; c0 += kTile) {
+        if (c0 > 0) __syncthreads();
+        if (c0 == 0) vpre.store(vt);
+        else {
+            KvTile<HD, F16> vv;
+            vv.load(a.vcache, pg, a.hkv, kvh, c0, n, t0);
+            vv.store(vt);
+        }
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile && tid >= HD && tid < 2 * HD)
+            vt[pos - t0 - c0][tid - HD] = cur_e;
+        __syncthreads();
+        const int lim = min(kTile, n - c0);
+        for (int j = sl; j < lim; j += NS) {
+            const u4_t vw = *reinterpret_cast<const u4_t*>(&vt[j][ch * 8]);
+            float v[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t w = dword_at(vw, i);
                 v[2 * i] = kv_decode<F16>(w & 0xffffu);
                 v[2 * i + 1] = kv_decode<F16>(w >> 16);
             }
-        }
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float p = sc[g][tl];
+            for (int g = 0; g < G; g++) {
+                const float p = sc[g][c0 + j];
 #pragma unroll
-            for (int i = 0; i < 8; i++) o[g][i] = fmaf(p, v[i], o[g][i]);
+                for (int i = 0; i < 8; i++) o[g][i] = fmaf(p, v[i], o[g][i]);
+            }
         }
     }
     const bool direct = a.n_splits == 1;
