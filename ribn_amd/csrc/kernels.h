@@ -43,8 +43,14 @@ struct SeqState {
 
 // The graphs read the active sequence through this indirection, so one
 // captured graph serves every sequence: the host swaps `seq` with a tiny copy.
+// The embedding kernel (first of every step) also copies the active
+// sequence's position and page-table pointer here, so later kernels of the
+// step reach them in one dependent load instead of two.
 struct StepCtl {
     SeqState* seq;
+    int32_t pos;
+    int32_t pad;
+    const int32_t* pages;
 };
 
 enum MvMode : int32_t {

@@ -197,6 +197,11 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(EmbedArgs a) {
     const int pos = s->pos;
     const uint32_t tok = s->tokens[pos];
     const int e = blockIdx.x * kThreads + threadIdx.x;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        StepCtl* c = const_cast<StepCtl*>(a.ctl);
+        c->pos = pos;
+        c->pages = s->pages;
+    }
     if (e < a.hidden) a.h[e] = deq_elem(a.w, tok, (uint32_t)e);
     if (blockIdx.x == 0 && (int)threadIdx.x < a.half_rot) {
         const float theta = (float)pos * a.inv_freq[threadIdx.x];
@@ -618,8 +623,20 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     __shared__ int pg[kMaxSplitTokens / kPageTokens];
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const SeqState* s = a.ctl->seq;
-    const int pos = s->pos, ctx = pos + 1;
+    const int qd = a.hq * HD, kd = a.hkv * HD;
+    float rawv[(G + 2 + (kThreads / HD) - 1) / (kThreads / HD)];   // q/k/v rows, loaded before the position
+#pragma unroll
+    for (int j = 0; j < (int)(sizeof(rawv) / sizeof(float)); j++) {
+        const int i = j * kThreads + tid;
+        if (i < (G + 2) * HD) {
+            const int r = i / HD, d = i % HD;
+            const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
+                                     : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
+            rawv[j] = src[d];
+        }
+    }
+    const int pos = a.ctl->pos, ctx = pos + 1;
+    const int32_t* pages = a.ctl->pages;
     int per = (ctx + a.n_splits - 1) / a.n_splits;
     per = (per + kPageTokens - 1) / kPageTokens * kPageTokens;
     if (per > kMaxSplitTokens) {
@@ -630,16 +647,14 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
         return;
     }
     const int t0 = split * per, t1 = min(ctx, t0 + per), n = max(0, t1 - t0);
-    const int qd = a.hq * HD, kd = a.hkv * HD;
     const bool owner = t0 <= pos && pos < t1;
 
     for (int i = tid; i < n; i += kThreads)
-        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = s->pages[(t0 + i) / kPageTokens];
-    for (int i = tid; i < (G + 2) * HD; i += kThreads) {
-        const int r = i / HD, d = i % HD;
-        const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
-                                 : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
-        buf[r][d] = src[d];
+        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = pages[(t0 + i) / kPageTokens];
+#pragma unroll
+    for (int j = 0; j < (int)(sizeof(rawv) / sizeof(float)); j++) {
+        const int i = j * kThreads + tid;
+        if (i < (G + 2) * HD) buf[i / HD][i % HD] = rawv[j];
     }
     __syncthreads();
     KvTile<HD, F16> kpre, vpre;   // first tile in flight during the prologue
@@ -690,7 +705,10 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
             kk.load(a.kcache, pg, a.hkv, kvh, c0, n, t0);
             kk.store(kt);
         }
-        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile && tid < HD) kt[pos - t0 - c0][tid] = cur_e;
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
+            __syncthreads();
+            if (tid < HD) kt[pos - t0 - c0][tid] = cur_e;
+        }
         __syncthreads();
         const int tl = c0 + stl;
         float acc[G];
@@ -755,8 +773,10 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
             vv.load(a.vcache, pg, a.hkv, kvh, c0, n, t0);
             vv.store(vt);
         }
-        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile && tid >= HD && tid < 2 * HD)
-            vt[pos - t0 - c0][tid - HD] = cur_e;
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
+            __syncthreads();
+            if (tid >= HD && tid < 2 * HD) vt[pos - t0 - c0][tid - HD] = cur_e;
+        }
         __syncthreads();
         const int lim = min(kTile, n - c0);
         for (int j = sl; j < lim; j += NS) {
@@ -799,27 +819,43 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     }
     if (!arrive_last(a.counters + kvh, a.n_splits)) return;
 
-    // -- merge the splits of this KV head (log-sum-exp in base 2)
+    // -- merge the splits of this KV head (log-sum-exp in base 2). The split
+    //    statistics are fetched in one parallel batch, then each output
+    //    element's partials with all loads issued before any is used.
     const float* base = a.part + (size_t)kvh * a.n_splits * REC;
+    float* smx = &sc[0][0];                        // [G][n_splits] maxima (scores are dead)
+    float* swt = &sc[0][0] + G * kMaxSplits;       // [G][n_splits] weights
+    for (int i = tid; i < G * a.n_splits; i += kThreads) {
+        const int g = i / a.n_splits, sp = i % a.n_splits;
+        smx[i] = ld_agent(base + (size_t)sp * REC + G * HD + g);
+        swt[i] = ld_agent(base + (size_t)sp * REC + G * HD + G + g);
+    }
+    __syncthreads();
     if (tid < G) {
         float mx = -INFINITY;
-        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, ld_agent(base + (size_t)sp * REC + G * HD + tid));
+        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, smx[tid * a.n_splits + sp]);
         float lt = 0.f;
         for (int sp = 0; sp < a.n_splits; sp++) {
-            const float ms = ld_agent(base + (size_t)sp * REC + G * HD + tid);
-            if (ms != -INFINITY) lt += ld_agent(base + (size_t)sp * REC + G * HD + G + tid) * exp2f(ms - mx);
+            const float ms = smx[tid * a.n_splits + sp];
+            const float wgt = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+            lt += swt[tid * a.n_splits + sp] * wgt;
+            swt[tid * a.n_splits + sp] = wgt;
         }
-        stat[0][tid] = mx;
         stat[1][tid] = lt;
     }
     __syncthreads();
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int g = idx / HD;
-        const float mx = stat[0][g];
+        const float* w8 = swt + g * a.n_splits;
         float acc = 0.f;
-        for (int sp = 0; sp < a.n_splits; sp++) {
-            const float ms = ld_agent(base + (size_t)sp * REC + G * HD + g);
-            if (ms != -INFINITY) acc += ld_agent(base + (size_t)sp * REC + idx) * exp2f(ms - mx);
+        for (int sp0 = 0; sp0 < a.n_splits; sp0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                v[j] = sp0 + j < a.n_splits ? ld_agent(base + (size_t)(sp0 + j) * REC + idx) : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (sp0 + j < a.n_splits) acc = fmaf(v[j], w8[sp0 + j], acc);
         }
         a.out[(size_t)kvh * G * HD + idx] = acc / stat[1][g];
     }

@@ -98,7 +98,7 @@ struct ribn_rocm_model {
     int32_t* d_pages = nullptr;
     uint32_t* d_tokens = nullptr;
     StepCtl* d_ctl = nullptr;
-    SeqState** h_slot_ptr = nullptr;   // pinned: &d_slots[i]
+    StepCtl* h_ctl = nullptr;          // pinned: per-slot StepCtl images
     SeqState* h_state = nullptr;        // pinned mirrors
     int32_t* h_pages = nullptr;
     uint32_t* h_tokens = nullptr;
@@ -410,7 +410,7 @@ hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
 
 // Point the graphs at `slot` and (re)write its device state from the pinned mirror.
 hipError_t select_slot(ribn_rocm_model* M, int slot) {
-    return hipMemcpyAsync(M->d_ctl, &M->h_slot_ptr[slot], sizeof(SeqState*), hipMemcpyHostToDevice, M->stream);
+    return hipMemcpyAsync(M->d_ctl, &M->h_ctl[slot], sizeof(StepCtl), hipMemcpyHostToDevice, M->stream);
 }
 
 hipError_t reset_slot(ribn_rocm_model* M, int slot, const std::vector<int32_t>& pages, const uint32_t* toks,
@@ -637,13 +637,15 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(dalloc(M, &M->d_ctl, sizeof(StepCtl)));
     HIPCHK(hipMemsetAsync(M->d_pages, 0, sizeof(int32_t) * (size_t)slots * M->max_pages, M->stream));
     HIPCHK(hipMemsetAsync(M->d_tokens, 0, sizeof(uint32_t) * (size_t)slots * (M->context + 1), M->stream));
-    HIPCHK(halloc(M, &M->h_slot_ptr, sizeof(SeqState*) * slots));
+    HIPCHK(halloc(M, &M->h_ctl, sizeof(StepCtl) * slots));
     HIPCHK(halloc(M, &M->h_state, sizeof(SeqState) * slots));
     HIPCHK(halloc(M, &M->h_pages, sizeof(int32_t) * (size_t)slots * M->max_pages));
     HIPCHK(halloc(M, &M->h_tokens, sizeof(uint32_t) * (size_t)slots * (M->context + 1)));
     HIPCHK(halloc(M, &M->h_out, sizeof(uint32_t) * (M->max_seqs + 8)));
     for (int s = 0; s < slots; s++) {
-        M->h_slot_ptr[s] = &M->d_slots[s];
+        M->h_ctl[s].seq = &M->d_slots[s];
+        M->h_ctl[s].pos = 0;
+        M->h_ctl[s].pages = M->d_pages + (size_t)s * M->max_pages;
         SeqState& st = M->h_state[s];
         st.pos = 0;
         st.last_token = 0;
@@ -653,7 +655,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         st.tokens = M->d_tokens + (size_t)s * (M->context + 1);
     }
     HIPCHK(hipMemcpyAsync(M->d_slots, M->h_state, sizeof(SeqState) * slots, hipMemcpyHostToDevice, M->stream));
-    HIPCHK(hipMemcpyAsync(M->d_ctl, &M->h_slot_ptr[slots - 1], sizeof(SeqState*), hipMemcpyHostToDevice, M->stream));
+    HIPCHK(hipMemcpyAsync(M->d_ctl, &M->h_ctl[slots - 1], sizeof(StepCtl), hipMemcpyHostToDevice, M->stream));
     HIPCHK(hipStreamSynchronize(M->stream));
     for (int s = (int)M->max_seqs - 1; s >= 0; s--) M->free_slots.push_back(s);
     for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
@@ -1161,6 +1163,7 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
         const uint32_t tok0 = 0;
         HIPCHK(reset_slot(M, slot, bench_pages, &tok0, 1));
         M->h_state[slot].pos = ctx - 1;
+        M->h_ctl[slot].pos = ctx - 1;   // no embedding kernel runs here to publish it
         HIPCHK(hipMemcpyAsync(&M->d_slots[slot], &M->h_state[slot], sizeof(SeqState), hipMemcpyHostToDevice, M->stream));
         HIPCHK(select_slot(M, slot));
         attn = true;
