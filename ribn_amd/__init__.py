@@ -24,7 +24,8 @@ from typing import Optional, Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "librocm_ribn.so")
+# RIBN_ROCM_LIB points at an alternative build of the same library (development only).
+LIB_PATH = os.environ.get("RIBN_ROCM_LIB") or os.path.join(_HERE, "librocm_ribn.so")
 
 GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 8, 12, 14
 BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210)}

@@ -13,12 +13,17 @@ constexpr int kMaxSplitTokens = 512;   // positions one attention workgroup cove
 // A quantized matrix after load-time re-tiling: `rows` output rows of `k`
 // inputs, GGML row n = input-contiguous. Each GGML block is split into
 // 16-byte-aligned planes so every wavefront load is a coalesced 128-bit load:
-//   Q4_K: a = qs   [rows][nb][128]   b = head [rows][nb][16] (d, dmin, 12 scale bytes)
+//   Q4_K: a = qs   [rows][nb][128]   b = scales [rows][nb][16]   c = d|dmin [rows][nb][4]
+//         (the twelve packed 6-bit scale/min bytes unpacked to one byte each,
+//          dword p = sc(2p), sc(2p+1), m(2p), m(2p+1): the pair lane p reads)
 //   Q6_K: a = ql   [rows][nb][128]   b = qh [rows][nb][64]
-//         c = sc   [rows][nb][16]    d = d  [rows][nb] (f16)
+//         c = sc   [rows][nb][16] reordered: byte 2c+slot holds sub-block scale
+//                  s = 8(c/4) + c%4 + 4 slot (the two scales unit c needs)
+//         d = d    [rows][nb] (f16)
 //   Q8_0: a = qs   [rows][nb][32]    b = d  [rows][nb] (f16)
-// The planes hold exactly the GGUF bytes (no requantization): bytes per block
-// are unchanged (144 / 210 / 34).
+// The planes hold exactly the GGUF values (no requantization). Q6_K and Q8_0
+// keep their block size (210 / 34 bytes); Q4_K grows from 144 to 148 bytes
+// per block because its 6-bit scales are stored unpacked.
 struct QMat {
     uint32_t type;
     uint32_t rows;

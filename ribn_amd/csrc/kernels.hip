@@ -5,12 +5,10 @@
 //  * weights stay in their GGUF block encoding, re-tiled at load into
 //    16-byte-aligned planes (kernels.h, QMat) so each lane issues 128-bit
 //    non-temporal loads and a wave reads 1 KiB of contiguous quants;
-//  * the input vector is staged once per workgroup in LDS as fp16 with a
-//    power-of-two scale, plus fp32 sums of every 16 staged values;
-//  * quants become fp16 by byte permutes (1024 + q has q in the low mantissa
-//    bits) and meet x in v_dot2_f32_f16 with fp32 accumulation; the constant
-//    1024 (and the Q6_K/Q8_0 offsets) is removed with the 16-element sums,
-//    and the Q4_K minimum term uses the same sums;
+//  * the input vector is staged once per workgroup in LDS as two int8 parts
+//    per value with one fp32 scale per 16 values (about 15 significant bits),
+//    and the quants meet it in v_dot4_i32_i8 with exact int32 accumulation;
+//    per-16 fp32 sums of x carry the Q4_K minimum and the Q6_K offset terms;
 //  * RMSNorm is a workgroup prologue; residual add, SwiGLU and the vocab argmax
 //    are epilogues; q/k head norm, NeoX rope and the KV append live in the
 //    attention prologue, so one layer is 5 launches.
@@ -25,7 +23,6 @@
 namespace ribn {
 namespace {
 
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
@@ -41,31 +38,6 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 __device__ __forceinline__ uint32_t byte_at(uint32_t v, uint32_t j) { return (v >> (8u * j)) & 0xffu; }
 __device__ __forceinline__ uint32_t dword_at(const u4_t& v, uint32_t i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-
-// Bytes b0..b3 of `v` (each < 256) -> two fp16 pairs (1024 + b0, 1024 + b1), (1024 + b2, 1024 + b3).
-__device__ __forceinline__ h2_t lo_pair(uint32_t v) {
-    return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
-}
-__device__ __forceinline__ h2_t hi_pair(uint32_t v) {
-    return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
-}
-__device__ __forceinline__ float fdot2(h2_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(a, __builtin_bit_cast(h2_t, b), c, false);
-}
-// sum_{j<16} (1024 + byte_j(q)) * x_j with x as 8 fp16 pairs in xa, xb.
-__device__ __forceinline__ float dot16(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& xa,
-                                       const u4_t& xb) {
-    float s = 0.f;
-    s = fdot2(lo_pair(q0), xa.x, s);
-    s = fdot2(hi_pair(q0), xa.y, s);
-    s = fdot2(lo_pair(q1), xa.z, s);
-    s = fdot2(hi_pair(q1), xa.w, s);
-    s = fdot2(lo_pair(q2), xb.x, s);
-    s = fdot2(hi_pair(q2), xb.y, s);
-    s = fdot2(lo_pair(q3), xb.z, s);
-    s = fdot2(hi_pair(q3), xb.w, s);
-    return s;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -156,27 +128,23 @@ __device__ float deq_elem(const QMat& w, uint32_t row, uint32_t e) {
         return __fmul_rn(d, (float)q);
     }
     if (w.type == 12) {
-        const uint8_t* h = w.b + bi * 16;
-        float d = canon_f16(h[0] | (h[1] << 8)), dmin = canon_f16(h[2] | (h[3] << 8));
-        const uint8_t* e12 = h + 4;
-        uint32_t g = i / 32, j = i % 32, sc, mn;
-        if (g < 4) {
-            sc = e12[g] & 63u;
-            mn = e12[4 + g] & 63u;
-        } else {
-            sc = (e12[8 + g - 4] & 15u) | ((e12[g - 4] >> 2) & 0x30u);
-            mn = (e12[8 + g - 4] >> 4) | ((e12[4 + g - 4] >> 2) & 0x30u);
-        }
+        // planes: a = qs, b = unpacked scales (dword p = sc(2p), sc(2p+1), m(2p), m(2p+1)), c = d | dmin
+        const uint8_t* dd = w.c + bi * 4;
+        float d = canon_f16(dd[0] | (dd[1] << 8)), dmin = canon_f16(dd[2] | (dd[3] << 8));
+        uint32_t g = i / 32, j = i % 32;
+        const uint8_t* sp = w.b + bi * 16 + (g / 2) * 4;
+        uint32_t sc = sp[g % 2], mn = sp[2 + g % 2];
         uint32_t q = (w.a[bi * 128 + (g / 2) * 32 + j] >> ((g % 2) * 4)) & 15u;
         float gs = __fmul_rn(d, (float)sc), gm = __fmul_rn(dmin, (float)mn);
         return __fsub_rn(__fmul_rn(gs, (float)q), gm);
     }
-    // Q6_K
+    // Q6_K: scale s of sub-block s is at byte 2c + slot, c = 4(s/8) + s%4, slot = (s/4)%2
     uint32_t g = i / 32, pos = i % 32, chunk = g / 4, variant = g % 4;
     uint32_t lo = (w.a[bi * 128 + chunk * 64 + (variant % 2) * 32 + pos] >> (variant < 2 ? 0 : 4)) & 15u;
     uint32_t hi = (w.b[bi * 64 + chunk * 32 + pos] >> (2 * variant)) & 3u;
     float d = canon_f16(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
-    int8_t sc = (int8_t)w.c[bi * 16 + g * 2 + pos / 16];
+    const uint32_t sidx = g * 2 + pos / 16;
+    int8_t sc = (int8_t)w.c[bi * 16 + 2 * (4 * (sidx / 8) + sidx % 4) + (sidx / 4) % 2];
     float gs = __fmul_rn(d, (float)sc);
     return __fmul_rn(gs, (float)((int)(lo | (hi << 4)) - 32));
 }
@@ -215,80 +183,126 @@ __global__ void advance_kernel(const StepCtl* ctl) {
 }
 
 // ---------------------------------------------------------------------------
-// Matvec input staging: x (optionally RMS-normalised, rms_norm model_ops.rs:108:
-// x * (1/sqrt(sum/n + eps)) * w) -> fp16 in LDS scaled by 2^e so that max|x|
-// lies in [2^14, 2^15), plus fp32 sums of each 16 staged values. Inputs up to
-// kStageF32 elements are read once (kept as fp32 in LDS between the statistics
-// and the conversion); longer ones are read twice. Returns 2^-e.
-constexpr int kStageF32 = 16384;
-
-// LDS layout of the matvec: [k] fp16 | [k/16] fp32 sums | 64 fp32 reduction
-// slots | (k <= kStageF32) [k] fp32 staging; 16-byte aligned pieces.
+// Matvec input staging. x (optionally the RMSNorm input: rms_norm model_ops.rs:108,
+// x * (1/sqrt(sum/n + eps)) * w) is cut into groups of 16 values; each group gets
+// an fp32 scale s = max|v|/127 and two int8 parts, v ~ s (hi + lo/256), i.e.
+// about 15 significant bits, and the fp32 sum X of its values (for the Q4_K
+// minima and the Q6_K offset). The products with the quants then run on
+// v_dot4_i32_i8 with exact int32 accumulation. For an RMSNorm input the group
+// holds x*w and the normalisation factor 1/sqrt(mean(x^2)+eps) is returned as
+// an output multiplier, so x is read once.
+//
+// LDS layout: [k] int8 parts in unit planes | [k/16] (s, X) pairs | 64 fp32
+// reduction slots. Unit planes: plane j (Q4_K/Q6_K: 0..3, Q8_0: 0..1) holds,
+// for every unit u of the value type, the 16 bytes that unit's lane reads j-th
+// (hi then lo of its first 16 values, then hi and lo of its second 16), so
+// lane i of a wave reads the i-th 16 bytes of a plane (no bank conflicts).
 __host__ __device__ constexpr size_t mv_red_offset(int k) {
-    return ((size_t)k * 2 + (size_t)(k / 16) * 4 + 15) / 16 * 16;
+    return ((size_t)k * 2 + (size_t)(k / 16) * 8 + 15) / 16 * 16;
 }
 
-__device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* xf, float* red) {
+// Unit, first plane (hi part; lo part in the next plane) and scale slot of the
+// 16 values x[16g .. 16g+16).
+template <int T>
+__device__ __forceinline__ void plane_of_group(int g, int& unit, int& plane, int& slot) {
+    if constexpr (T == 8) {
+        unit = g; plane = 0; slot = 0;
+    } else if constexpr (T == 12) {
+        const int blk = g >> 4, o = (g & 15) * 16, grp = o >> 5, hf = (o & 31) >> 4;
+        unit = blk * 8 + (grp >> 1) * 2 + hf;
+        plane = (grp & 1) * 2;
+        slot = grp & 1;
+    } else {
+        const int blk = g >> 4, o = (g & 15) * 16, chunk = o >> 7, v = (o & 127) >> 5, hf = (o & 31) >> 4;
+        unit = blk * 8 + chunk * 4 + (v & 1) * 2 + hf;
+        plane = (v >> 1) * 2;
+        slot = v >> 1;
+    }
+}
+
+template <int T>
+__device__ float stage_x(const MvArgs& a, int8_t* xs, float* gs, float* red) {
     const int k = a.k, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
     const bool norm = a.norm_w != nullptr;
-    const bool keep = k <= kStageF32;
-    float4* xf4 = reinterpret_cast<float4*>(xf);
-    float ss = 0.f, am = 0.f;
-    for (int i = tid; i < k / 4; i += kThreads) {
-        float4 v = x4[i];
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        if (norm) {
-            const float4 w = w4[i];
-            v.x *= w.x; v.y *= w.y; v.z *= w.z; v.w *= w.w;   // x*w; inv is applied below
-        }
-        am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        if (keep) xf4[i] = v;
-    }
-    ss = wave_sum(ss);
-    am = wave_max(am);
-    if (lane == 0) { red[wave] = ss; red[kWaves + wave] = am; }
-    __syncthreads();
-    ss = 0.f; am = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWaves; i++) { ss += red[i]; am = fmaxf(am, red[kWaves + i]); }
-    const float inv = norm ? 1.0f / sqrtf(ss / (float)k + a.eps) : 1.0f;
-    const float amax = am * inv * 1.0001f;
-    int ex = 0;
-    if (amax > 0.f && amax < 3.0e38f) frexpf(amax, &ex);
-    ex = min(max(15 - ex, -100), 100);
-    const float scale = ldexpf(1.0f, ex);
+    const int n_units = T == 8 ? k / 16 : k / 32;
+    u4_t* planes = reinterpret_cast<u4_t*>(xs);
+    float ss = 0.f;
     for (int g = tid; g < k / 16; g += kThreads) {
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float4 t;
-            if (keep) {
-                t = xf4[g * 4 + j];
-            } else {
-                t = x4[g * 4 + j];
-                if (norm) {
-                    const float4 w = w4[g * 4 + j];
-                    t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
-                }
+            float4 t = x4[g * 4 + j];
+            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+            if (norm) {
+                const float4 w = w4[g * 4 + j];
+                t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
             }
             v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
         }
-        float sum = 0.f;
-        _Float16 hv[16];
+        float am = 0.f, sum = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            hv[j] = (_Float16)(v[j] * inv * scale);
-            sum += (float)hv[j];
+            am = fmaxf(am, fabsf(v[j]));
+            sum += v[j];
         }
-        u4_t* dst = reinterpret_cast<u4_t*>(xs + g * 16);
-        dst[0] = *reinterpret_cast<u4_t*>(&hv[0]);
-        dst[1] = *reinterpret_cast<u4_t*>(&hv[8]);
-        gs[g] = sum;
+        const float sc = am * (1.0f / 127.0f);
+        const float is = am > 0.f ? 127.0f / am : 0.f;
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t h4 = 0, l4 = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float vv = v[4 * j + b];
+                const float hq = rintf(vv * is);
+                const float lq = fminf(fmaxf(rintf((vv - hq * sc) * is * 256.0f), -127.f), 127.f);
+                h4 |= ((uint32_t)(int32_t)hq & 0xffu) << (8 * b);
+                l4 |= ((uint32_t)(int32_t)lq & 0xffu) << (8 * b);
+            }
+            hw[j] = h4;
+            lw[j] = l4;
+        }
+        int unit, plane, slot;
+        plane_of_group<T>(g, unit, plane, slot);
+        planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
+        planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
+        if constexpr (T == 8) {
+            gs[unit * 2] = sc;
+            gs[unit * 2 + 1] = sum;
+        } else {
+            gs[unit * 4 + slot] = sc;
+            gs[unit * 4 + 2 + slot] = sum;
+        }
+    }
+    float inv = 1.0f;
+    if (norm) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) ss += red[i];
+        inv = 1.0f / sqrtf(ss / (float)k + a.eps);
     }
     __syncthreads();
-    return 1.0f / scale;
+    return inv;
+}
+
+// sum_j q_j x_j over 16 values for int8 bytes q (4 per dword) and x parts.
+__device__ __forceinline__ int dot16i(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& x) {
+    int acc = __builtin_amdgcn_sdot4((int)q0, (int)x.x, 0, false);
+    acc = __builtin_amdgcn_sdot4((int)q1, (int)x.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)q2, (int)x.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)q3, (int)x.w, acc, false);
+    return acc;
+}
+// s * sum_j q_j v_j for a group staged as v ~ s (hi + lo/256)
+__device__ __forceinline__ float dot16s(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& xh,
+                                        const u4_t& xl) {
+    const int h = dot16i(q0, q1, q2, q3, xh), l = dot16i(q0, q1, q2, q3, xl);
+    return fmaf((float)l, 1.0f / 256.0f, (float)h);
 }
 
 // ---------------------------------------------------------------------------
@@ -298,46 +312,60 @@ __device__ float stage_x(const MvArgs& a, _Float16* xs, float* gs, float* xf, fl
 //  Q6_K: 8 units per block; unit c holds ql bytes 16c..16c+15: low nibbles are
 //        group 4*(c/4) + (c/2)%2, high nibbles that group + 2 (lib.rs:623-649).
 //  Q8_0: 2 units per block (16 int8 each).
+// A wave walks 128 consecutive units of a row per load group (two halves of 64:
+// lane l takes units g0 + l and g0 + 64 + l), so every row offset is
+// wave-uniform and only the lane's fixed offset lives in a vector register.
+__device__ __forceinline__ uint32_t ld_nt32(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+__device__ __forceinline__ uint32_t ld_nt16b(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+}
+
+// base: wave-uniform pointer (scalar registers); off: the lane's 32-bit byte
+// offset, so the load uses scalar-base + vector-offset addressing.
+__device__ __forceinline__ u4_t ldo_nt16(const uint8_t* base, uint32_t off) { return ld_nt16(base + off); }
+
 template <int T>
 struct Unit;
 
 template <>
 struct Unit<12> {
     static constexpr int kPerBlock = 8;
-    struct Raw { u4_t q, h; };
+    struct Raw { u4_t q; uint32_t s, dd; };
+    // unit u of `row`: quants, the lane's scale dword [sc(2p), sc(2p+1), m(2p), m(2p+1)], d|dmin
     static __device__ __forceinline__ Raw load(const QMat& w, size_t row, int u) {
-        const size_t nb = w.nb;
+        const size_t bi = row * w.nb + (u >> 3);
         Raw r;
-        r.q = ld_nt16(w.a + (row * nb * 128) + (size_t)u * 16);
-        r.h = ld16(w.b + (row * nb + (u >> 3)) * 16);
+        r.q = ld_nt16(w.a + row * w.nb * 128 + (size_t)u * 16);
+        r.s = ld_nt32(w.b + bi * 16 + ((u & 7) >> 1) * 4);
+        r.dd = ld_nt32(w.c + bi * 4);
         return r;
     }
-    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, const float* gs, float acc) {
-        const int blk = u >> 3, c = u & 7, p = c >> 1, hf = c & 1;
-        const uint32_t g0 = 2 * p, g1 = 2 * p + 1;
-        uint32_t sc0, sc1, m0, m1;
-        if (p < 2) {
-            sc0 = byte_at(r.h.y, g0) & 63u; sc1 = byte_at(r.h.y, g1) & 63u;
-            m0 = byte_at(r.h.z, g0) & 63u;  m1 = byte_at(r.h.z, g1) & 63u;
-        } else {
-            const uint32_t j0 = g0 - 4, j1 = g1 - 4;
-            sc0 = (byte_at(r.h.w, j0) & 15u) | ((byte_at(r.h.y, j0) >> 2) & 0x30u);
-            sc1 = (byte_at(r.h.w, j1) & 15u) | ((byte_at(r.h.y, j1) >> 2) & 0x30u);
-            m0 = (byte_at(r.h.w, j0) >> 4) | ((byte_at(r.h.z, j0) >> 2) & 0x30u);
-            m1 = (byte_at(r.h.w, j1) >> 4) | ((byte_at(r.h.z, j1) >> 2) & 0x30u);
-        }
-        const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
-        const int xo = blk * 256 + 64 * p + 16 * hf;   // in halves
-        const u4_t xa = xs4[xo / 8], xb = xs4[xo / 8 + 1];
-        const u4_t ya = xs4[xo / 8 + 4], yb = xs4[xo / 8 + 5];
-        const float X0 = gs[xo / 16], X1 = gs[xo / 16 + 2];
+    // units g0 + lane (g0 a multiple of 64, wave-uniform)
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        const size_t bi0 = row * w.nb + (size_t)(g0 >> 3);
+        const uint8_t* qa = w.a + (row * w.nb * 128 + (size_t)g0 * 16);
+        const uint8_t* sb = w.b + bi0 * 16;
+        const uint8_t* dc = w.c + bi0 * 4;
+        Raw r;
+        r.q = ld_nt16(qa + (uint32_t)(lane * 16));
+        r.s = ld_nt32(sb + (uint32_t)((lane >> 3) * 16 + ((lane & 7) >> 1) * 4));
+        r.dd = ld_nt32(dc + (uint32_t)((lane >> 3) * 4));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const float4 G = reinterpret_cast<const float4*>(gs)[u];   // s_a, s_b, X_a, X_b
         const uint32_t m = 0x0f0f0f0fu;
-        const float s0 = dot16(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m, xa, xb);
-        const float s1 = dot16((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m, ya, yb);
-        acc = fmaf(d * (float)sc0, fmaf(-1024.f, X0, s0), acc);
-        acc = fmaf(d * (float)sc1, fmaf(-1024.f, X1, s1), acc);
-        acc = fmaf(-dmin * (float)m0, X0, acc);
-        acc = fmaf(-dmin * (float)m1, X1, acc);
+        const float t0 = dot16s(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m, xs4[u], xs4[U + u]);
+        const float t1 = dot16s((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m, xs4[2 * U + u],
+                                xs4[3 * U + u]);
+        // sum_j x_j ((d sc) q_j - dmin m) = (d sc) s t - (dmin m) X, per group
+        acc = fmaf(d * (float)(r.s & 0xffu) * G.x, t0, acc);
+        acc = fmaf(-dmin * (float)((r.s >> 16) & 0xffu), G.z, acc);
+        acc = fmaf(d * (float)((r.s >> 8) & 0xffu) * G.y, t1, acc);
+        acc = fmaf(-dmin * (float)(r.s >> 24), G.w, acc);
         return acc;
     }
 };
@@ -345,38 +373,46 @@ struct Unit<12> {
 template <>
 struct Unit<14> {
     static constexpr int kPerBlock = 8;
-    struct Raw { u4_t ql, qh; int32_t sl, sh; uint32_t d; };
+    struct Raw { u4_t ql, qh; uint32_t sc, d; };
     static __device__ __forceinline__ Raw load(const QMat& w, size_t row, int u) {
-        const size_t nb = w.nb, bi = row * nb + (u >> 3);
-        const int c = u & 7, il = ((c >> 2) * 4 + ((c >> 1) & 1)) * 2 + (c & 1);
+        const size_t bi = row * w.nb + (u >> 3);
+        const int c = u & 7;
         Raw r;
-        r.ql = ld_nt16(w.a + row * nb * 128 + (size_t)u * 16);
+        r.ql = ld_nt16(w.a + row * w.nb * 128 + (size_t)u * 16);
         r.qh = ld_nt16(w.b + bi * 64 + 16 * (2 * (c >> 2) + (c & 1)));
-        r.sl = *reinterpret_cast<const int8_t*>(w.c + bi * 16 + il);
-        r.sh = *reinterpret_cast<const int8_t*>(w.c + bi * 16 + il + 4);
-        r.d = *reinterpret_cast<const uint16_t*>(w.d + bi * 2);
+        r.sc = ld_nt16b(w.c + bi * 16 + 2 * c);
+        r.d = ld_nt16b(w.d + bi * 2);
         return r;
     }
-    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, const float* gs, float acc) {
-        const int blk = u >> 3, c = u & 7, chunk = c >> 2, vb = (c >> 1) & 1, hf = c & 1;
-        const uint32_t sl = 2 * vb, sh = 2 * vb + 4;
-        const uint32_t m4 = 0x0f0f0f0fu, m2 = 0x03030303u;
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        const size_t bi0 = row * w.nb + (size_t)(g0 >> 3);
+        const int c = lane & 7;
+        Raw r;
+        r.ql = ld_nt16(w.a + (row * w.nb * 128 + (size_t)g0 * 16) + (uint32_t)(lane * 16));
+        r.qh = ld_nt16(w.b + bi0 * 64 + (uint32_t)((lane >> 3) * 64 + 16 * (2 * (c >> 2) + (c & 1))));
+        r.sc = ld_nt16b(w.c + bi0 * 16 + (uint32_t)((lane >> 3) * 16 + 2 * c));
+        r.d = ld_nt16b(w.d + bi0 * 2 + (uint32_t)((lane >> 3) * 2));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const int vb = ((u & 7) >> 1) & 1;
+        const uint32_t s1 = 4 - 2 * vb, s2 = 2 * vb;
+        const uint32_t m4 = 0x0f0f0f0fu, m30 = 0x30303030u;
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t l = dword_at(r.ql, i), h = dword_at(r.qh, i);
-            lo[i] = (l & m4) | (((h >> sl) & m2) << 4);
-            hi[i] = ((l >> 4) & m4) | (((h >> sh) & m2) << 4);
+            lo[i] = (l & m4) | ((h << s1) & m30);
+            hi[i] = ((l >> 4) & m4) | ((h >> s2) & m30);
         }
         const float d = h2f(r.d);
-        const int xo = blk * 256 + chunk * 128 + vb * 32 + 16 * hf;
-        const u4_t xa = xs4[xo / 8], xb = xs4[xo / 8 + 1];
-        const u4_t ya = xs4[xo / 8 + 8], yb = xs4[xo / 8 + 9];
-        const float X0 = gs[xo / 16], X1 = gs[xo / 16 + 4];
-        const float s0 = dot16(lo[0], lo[1], lo[2], lo[3], xa, xb);
-        const float s1 = dot16(hi[0], hi[1], hi[2], hi[3], ya, yb);
-        acc = fmaf(d * (float)r.sl, fmaf(-1056.f, X0, s0), acc);
-        acc = fmaf(d * (float)r.sh, fmaf(-1056.f, X1, s1), acc);
+        const float scl = (float)(int8_t)(r.sc & 0xffu), sch = (float)(int8_t)(r.sc >> 8);
+        const float4 G = reinterpret_cast<const float4*>(gs)[u];
+        const float t0 = dot16s(lo[0], lo[1], lo[2], lo[3], xs4[u], xs4[U + u]);
+        const float t1 = dot16s(hi[0], hi[1], hi[2], hi[3], xs4[2 * U + u], xs4[3 * U + u]);
+        // sum_j x_j (d sc)(q_j - 32) = (d sc)(s t - 32 X), per 16-value sub-block
+        acc = fmaf(d * scl, fmaf(G.x, t0, -32.0f * G.z), acc);
+        acc = fmaf(d * sch, fmaf(G.y, t1, -32.0f * G.w), acc);
         return acc;
     }
 };
@@ -386,17 +422,21 @@ struct Unit<8> {
     static constexpr int kPerBlock = 2;
     struct Raw { u4_t q; uint32_t d; };
     static __device__ __forceinline__ Raw load(const QMat& w, size_t row, int u) {
-        const size_t nb = w.nb;
         Raw r;
-        r.q = ld_nt16(w.a + row * nb * 32 + (size_t)u * 16);
-        r.d = *reinterpret_cast<const uint16_t*>(w.b + (row * nb + (u >> 1)) * 2);
+        r.q = ld_nt16(w.a + row * w.nb * 32 + (size_t)u * 16);
+        r.d = ld_nt16b(w.b + (row * w.nb + (u >> 1)) * 2);
         return r;
     }
-    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, const float* gs, float acc) {
-        const uint32_t f = 0x80808080u;
-        const int xo = u * 16;
-        const float s = dot16(r.q.x ^ f, r.q.y ^ f, r.q.z ^ f, r.q.w ^ f, xs4[xo / 8], xs4[xo / 8 + 1]);
-        return fmaf(h2f(r.d), fmaf(-1152.f, gs[u], s), acc);
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        Raw r;
+        r.q = ld_nt16(w.a + (row * w.nb * 32 + (size_t)g0 * 16) + (uint32_t)(lane * 16));
+        r.d = ld_nt16b(w.b + (row * w.nb + (size_t)(g0 >> 1)) * 2 + (uint32_t)((lane >> 1) * 2));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const float2 G = reinterpret_cast<const float2*>(gs)[u];
+        const float t = dot16s(r.q.x, r.q.y, r.q.z, r.q.w, xs4[u], xs4[U + u]);
+        return fmaf(h2f(r.d) * G.x, t, acc);
     }
 };
 
@@ -409,6 +449,7 @@ struct Group {
 // Where a wave's work lives: items (two rows each, or one gate/up pair) of one
 // segment, walked as a flat sequence of load groups so that the next group's
 // 128-bit loads are always in flight while the current group is computed.
+// Every field is wave-uniform.
 struct WaveWork {
     const QMat* wa;
     const QMat* wb;        // second row's matrix (the up matrix for gate/up pairs)
@@ -416,47 +457,55 @@ struct WaveWork {
     bool pair;
 };
 
-template <int T>
-__device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int q) {
+template <int T, bool FULL>
+__device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int it, int gi) {
     using U = Unit<T>;
-    const int it = q / w.ngr, gi = q % w.ngr;
     const int item = w.first_item + it * kWaves;
     const int ra = w.pair ? item : 2 * item;
     const int rb = w.pair ? item : min(ra + 1, w.n_rows - 1);
     const int lane = threadIdx.x & 63;
-    int u0 = gi * 128 + lane, u1 = u0 + 64;
-    u0 = u0 < w.n_units ? u0 : 0;
-    u1 = u1 < w.n_units ? u1 : 0;
-    g.a0 = U::load(*w.wa, (size_t)ra, u0);
-    g.b0 = U::load(*w.wb, (size_t)rb, u0);
-    g.a1 = U::load(*w.wa, (size_t)ra, u1);
-    g.b1 = U::load(*w.wb, (size_t)rb, u1);
+    if constexpr (FULL) {
+        g.a0 = U::load_full(*w.wa, (size_t)ra, gi * 128, lane);
+        g.b0 = U::load_full(*w.wb, (size_t)rb, gi * 128, lane);
+        g.a1 = U::load_full(*w.wa, (size_t)ra, gi * 128 + 64, lane);
+        g.b1 = U::load_full(*w.wb, (size_t)rb, gi * 128 + 64, lane);
+    } else {
+        int u0 = gi * 128 + lane, u1 = u0 + 64;
+        u0 = u0 < w.n_units ? u0 : 0;
+        u1 = u1 < w.n_units ? u1 : 0;
+        g.a0 = U::load(*w.wa, (size_t)ra, u0);
+        g.b0 = U::load(*w.wb, (size_t)rb, u0);
+        g.a1 = U::load(*w.wa, (size_t)ra, u1);
+        g.b1 = U::load(*w.wb, (size_t)rb, u1);
+    }
 }
 
-template <int T, int MODE>
+template <int T, int MODE, bool FULL>
 __device__ __forceinline__ void mv_body(const MvArgs& a, const MvSeg& sg, const WaveWork& w, Group<T>& cur,
                                         const u4_t* xs4, const float* gs, float oscale, uint64_t& best) {
     using U = Unit<T>;
     const int lane = threadIdx.x & 63;
     const int total = w.n_items * w.ngr;
     float a0 = 0.f, b0 = 0.f;
+    int it = 0, gi = 0;
     for (int q = 0; q < total; q++) {
+        const int gi2 = gi + 1 < w.ngr ? gi + 1 : 0;
+        const int it2 = gi + 1 < w.ngr ? it : it + 1;
         Group<T> nxt;
-        if (q + 1 < total) load_group<T>(nxt, w, q + 1);
-        const int gi = q % w.ngr;
+        if (q + 1 < total) load_group<T, FULL>(nxt, w, it2, gi2);
         const int u0 = gi * 128 + lane, u1 = u0 + 64;
-        if (u0 < w.n_units) {
-            a0 = U::apply(cur.a0, u0, xs4, gs, a0);
-            b0 = U::apply(cur.b0, u0, xs4, gs, b0);
+        if (FULL || u0 < w.n_units) {
+            a0 = U::apply(cur.a0, u0, xs4, w.n_units, gs, a0);
+            b0 = U::apply(cur.b0, u0, xs4, w.n_units, gs, b0);
         }
-        if (u1 < w.n_units) {
-            a0 = U::apply(cur.a1, u1, xs4, gs, a0);
-            b0 = U::apply(cur.b1, u1, xs4, gs, b0);
+        if (FULL || u1 < w.n_units) {
+            a0 = U::apply(cur.a1, u1, xs4, w.n_units, gs, a0);
+            b0 = U::apply(cur.b1, u1, xs4, w.n_units, gs, b0);
         }
         if (gi == w.ngr - 1) {
             float ya = wave_sum(a0) * oscale, yb = wave_sum(b0) * oscale;
             a0 = b0 = 0.f;
-            const int item = w.first_item + (q / w.ngr) * kWaves;
+            const int item = w.first_item + it * kWaves;
             const int ra = w.pair ? item : 2 * item;
             const int rb = w.pair ? item : ra + 1;
             if (lane == 0) {
@@ -480,8 +529,27 @@ __device__ __forceinline__ void mv_body(const MvArgs& a, const MvSeg& sg, const 
                 }
             }
         }
-        if (q + 1 < total) cur = nxt;
+        cur = nxt;
+        it = it2;
+        gi = gi2;
     }
+}
+
+template <int T, int MODE>
+__device__ __forceinline__ void mv_run(const MvArgs& a, const MvSeg& sg, WaveWork& w, int8_t* xs, float* gs,
+                                       float* red, uint64_t& best) {
+    w.n_units = (int)sg.w.nb * Unit<T>::kPerBlock;
+    w.ngr = (w.n_units + 127) / 128;
+    const bool full = (w.n_units & 127) == 0;
+    Group<T> g;
+    if (w.n_items > 0) {
+        if (full) load_group<T, true>(g, w, 0, 0);
+        else load_group<T, false>(g, w, 0, 0);
+    }
+    const float oscale = stage_x<T>(a, xs, gs, red);
+    const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
+    if (full) mv_body<T, MODE, true>(a, sg, w, g, xs4, gs, oscale, best);
+    else mv_body<T, MODE, false>(a, sg, w, g, xs4, gs, oscale, best);
 }
 
 // Fused dequant-matvec (gguf_gemv qwen_reference.rs:31-40; q*_gemv_warp
@@ -491,11 +559,9 @@ __device__ __forceinline__ void mv_body(const MvArgs& a, const MvSeg& sg, const 
 template <int TA, int TB, int MODE>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    _Float16* xs = reinterpret_cast<_Float16*>(lds);
+    int8_t* xs = reinterpret_cast<int8_t*>(lds);
     float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
     float* red = reinterpret_cast<float*>(lds + mv_red_offset(a.k));
-    float* xf = red + 64;
-    const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
 
     const int wg = blockIdx.x;
     int si = 0;
@@ -503,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     if (a.nseg > 2 && wg >= a.seg[2].wg_begin) si = 2;
     const MvSeg& sg = a.seg[si];
     const int lwg = wg - sg.wg_begin;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     constexpr bool pair = MODE == MV_SILU;
     WaveWork w;
     w.wa = &sg.w;
@@ -514,22 +580,8 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
     w.n_items = max(0, min(a.items_per_wave, (n_item_total - w.first_item + kWaves - 1) / kWaves));
     uint64_t best = 0ull;
-    const bool second = si == 2 && TB != TA;
-    if (!second) {
-        w.n_units = (int)sg.w.nb * Unit<TA>::kPerBlock;
-        w.ngr = (w.n_units + 127) / 128;
-        Group<TA> g;
-        if (w.n_items > 0) load_group<TA>(g, w, 0);
-        const float oscale = stage_x(a, xs, gs, xf, red);
-        mv_body<TA, MODE>(a, sg, w, g, xs4, gs, oscale, best);
-    } else {
-        w.n_units = (int)sg.w.nb * Unit<TB>::kPerBlock;
-        w.ngr = (w.n_units + 127) / 128;
-        Group<TB> g;
-        if (w.n_items > 0) load_group<TB>(g, w, 0);
-        const float oscale = stage_x(a, xs, gs, xf, red);
-        mv_body<TB, MODE>(a, sg, w, g, xs4, gs, oscale, best);
-    }
+    if (si == 2 && TB != TA) mv_run<TB, MODE>(a, sg, w, xs, gs, red, best);
+    else mv_run<TA, MODE>(a, sg, w, xs, gs, red, best);
 
     if constexpr (MODE == MV_HEAD) {
         // Greedy token: first maximum over the vocabulary, NaN skipped (model_ops.rs:203-260).
@@ -911,10 +963,15 @@ template <int MODE>
 hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
     const size_t lds = matvec_lds_bytes(a.k);
     const uint32_t ta = a.type_a, tb = a.nseg > 2 ? a.type_b : a.type_a;
-#define RIBN_MV(A, B)                                                             \
-    if (ta == A && tb == B) {                                                     \
-        matvec_kernel<A, B, MODE><<<n_wg, kThreads, lds, st>>>(a);                \
-        return hipGetLastError();                                                 \
+#define RIBN_MV(A, B)                                                                              \
+    if (ta == A && tb == B) {                                                                      \
+        if (lds > 65536) {                                                                         \
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_kernel<A, B, MODE>), \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+            if (e != hipSuccess) return e;                                                         \
+        }                                                                                          \
+        matvec_kernel<A, B, MODE><<<n_wg, kThreads, lds, st>>>(a);                                 \
+        return hipGetLastError();                                                                  \
     }
     if constexpr (MODE == MV_STORE) {
         RIBN_MV(12, 14) RIBN_MV(14, 12) RIBN_MV(12, 8) RIBN_MV(8, 12) RIBN_MV(14, 8) RIBN_MV(8, 14)
@@ -926,11 +983,7 @@ hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
 
 }  // namespace
 
-size_t matvec_lds_bytes(int k) {
-    size_t b = mv_red_offset(k) + 64 * 4;
-    if (k <= kStageF32) b += (size_t)k * 4;
-    return b;
-}
+size_t matvec_lds_bytes(int k) { return mv_red_offset(k) + 64 * 4; }
 
 int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * kWaves * (a.mode == MV_SILU ? 1 : 2); }
 

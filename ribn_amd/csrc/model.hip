@@ -161,14 +161,34 @@ void retile(uint32_t type, const uint8_t* src, uint64_t n_blocks, uint8_t* a, ui
     auto work = [&](uint64_t b0, uint64_t b1) {
         for (uint64_t i = b0; i < b1; i++) {
             if (type == GGML_Q4_K) {
+                // scale unpacking as q4_k_scales (crates/gguf/src/lib.rs:561-575)
                 const uint8_t* s = src + i * 144;
-                std::memcpy(b + i * 16, s, 16);
+                const uint8_t* e = s + 4;
+                uint8_t sc[8], mn[8];
+                for (int j = 0; j < 4; j++) {
+                    sc[j] = e[j] & 0x3f;
+                    sc[j + 4] = (uint8_t)((e[8 + j] & 0x0f) | ((e[j] >> 2) & 0x30));
+                    mn[j] = e[4 + j] & 0x3f;
+                    mn[j + 4] = (uint8_t)((e[8 + j] >> 4) | ((e[4 + j] >> 2) & 0x30));
+                }
+                uint8_t* o = b + i * 16;
+                for (int p = 0; p < 4; p++) {
+                    o[4 * p] = sc[2 * p];
+                    o[4 * p + 1] = sc[2 * p + 1];
+                    o[4 * p + 2] = mn[2 * p];
+                    o[4 * p + 3] = mn[2 * p + 1];
+                }
+                std::memcpy(c + i * 4, s, 4);
                 std::memcpy(a + i * 128, s + 16, 128);
             } else if (type == GGML_Q6_K) {
                 const uint8_t* s = src + i * 210;
                 std::memcpy(a + i * 128, s, 128);
                 std::memcpy(b + i * 64, s + 128, 64);
-                std::memcpy(c + i * 16, s + 192, 16);
+                for (int cc = 0; cc < 8; cc++) {
+                    const int il = 8 * (cc / 4) + cc % 4;
+                    c[i * 16 + 2 * cc] = s[192 + il];
+                    c[i * 16 + 2 * cc + 1] = s[192 + il + 4];
+                }
                 std::memcpy(d + i * 2, s + 208, 2);
             } else {
                 const uint8_t* s = src + i * 34;
@@ -190,7 +210,7 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 // Plane sizes for a [rows][k] matrix of `type`.
 void plane_sizes(uint32_t type, uint64_t nblocks, size_t* sa, size_t* sb, size_t* sc, size_t* sd) {
     *sa = *sb = *sc = *sd = 0;
-    if (type == GGML_Q4_K) { *sa = nblocks * 128; *sb = nblocks * 16; }
+    if (type == GGML_Q4_K) { *sa = nblocks * 128; *sb = nblocks * 16; *sc = nblocks * 4; }
     else if (type == GGML_Q6_K) { *sa = nblocks * 128; *sb = nblocks * 64; *sc = nblocks * 16; *sd = nblocks * 2; }
     else { *sa = nblocks * 32; *sb = nblocks * 2; }
 }
@@ -267,6 +287,14 @@ int layout_segments(MvArgs& a) {
     return wg;
 }
 
+// Development knob: RIBN_IPW_<KIND> overrides the items per wave of one launch kind.
+int ipw_env(const char* kind, int dflt) {
+    const std::string key = std::string("RIBN_IPW_") + kind;
+    const char* v = std::getenv(key.c_str());
+    const int x = v ? std::atoi(v) : 0;
+    return x >= 1 && x <= 16 ? x : dflt;
+}
+
 void build_launches(ribn_rocm_model* M) {
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
     M->mv_qkv.clear(); M->mv_o.clear(); M->mv_gu.clear(); M->mv_down.clear();
@@ -274,7 +302,7 @@ void build_launches(ribn_rocm_model* M) {
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
-        q.items_per_wave = 2;
+        q.items_per_wave = ipw_env("QKV", 2);
         q.nseg = 3;
         q.type_a = y.q.type;
         q.type_b = y.v.type;
@@ -288,7 +316,7 @@ void build_launches(ribn_rocm_model* M) {
         o.nseg = 1;
         o.seg[0].w = y.o; o.seg[0].out = M->h;
         o.type_a = o.type_b = y.o.type;
-        o.items_per_wave = 2;
+        o.items_per_wave = ipw_env("O", 2);
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
 
@@ -296,7 +324,7 @@ void build_launches(ribn_rocm_model* M) {
         g.nseg = 1;
         g.seg[0].w = y.gate; g.seg[0].w2 = y.up; g.seg[0].out = M->act;
         g.type_a = g.type_b = y.gate.type;
-        g.items_per_wave = 4;
+        g.items_per_wave = ipw_env("GU", 4);
         M->wg_gu.push_back(layout_segments(g));
         M->mv_gu.push_back(g);
 
@@ -304,7 +332,7 @@ void build_launches(ribn_rocm_model* M) {
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
         d.type_a = d.type_b = y.down.type;
-        d.items_per_wave = 2;
+        d.items_per_wave = ipw_env("DOWN", 2);
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
@@ -312,7 +340,7 @@ void build_launches(ribn_rocm_model* M) {
     hdv.nseg = 1;
     hdv.seg[0].w = M->out; hdv.seg[0].out = M->logits;
     hdv.type_a = hdv.type_b = M->out.type;
-    hdv.items_per_wave = choose_ipw(M->V / 2, 8);
+    hdv.items_per_wave = ipw_env("HEAD", choose_ipw(M->V / 2, 8));
     hdv.head.partial = M->head_partial;
     hdv.head.counter = M->counters + M->hkv;
     M->head_wgs = layout_segments(hdv);
@@ -1010,7 +1038,7 @@ hipError_t upload_plain(Scoped& S, uint32_t type, uint64_t rows, uint64_t k, con
         for (size_t i = 0; i < total; i++) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; host[i] = (uint8_t)x; }
         auto put_half = [](uint8_t* p, uint16_t h) { p[0] = (uint8_t)h; p[1] = (uint8_t)(h >> 8); };
         for (uint64_t i = 0; i < nblocks; i++) {
-            if (type == GGML_Q4_K) { put_half(hb + i * 16, 0x2000); put_half(hb + i * 16 + 2, 0x2000); }
+            if (type == GGML_Q4_K) { put_half(hc + i * 4, 0x2000); put_half(hc + i * 4 + 2, 0x2000); }
             else if (type == GGML_Q6_K) put_half(hd + i * 2, 0x2000);
             else put_half(hb + i * 2, 0x2000);
         }
