@@ -302,7 +302,7 @@ void build_launches(ribn_rocm_model* M) {
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
-        q.items_per_wave = ipw_env("QKV", 2);
+        q.items_per_wave = ipw_env("QKV", 1);
         q.nseg = 3;
         q.type_a = y.q.type;
         q.type_b = y.v.type;
@@ -316,7 +316,7 @@ void build_launches(ribn_rocm_model* M) {
         o.nseg = 1;
         o.seg[0].w = y.o; o.seg[0].out = M->h;
         o.type_a = o.type_b = y.o.type;
-        o.items_per_wave = ipw_env("O", 2);
+        o.items_per_wave = ipw_env("O", 1);
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
 
@@ -332,7 +332,7 @@ void build_launches(ribn_rocm_model* M) {
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
         d.type_a = d.type_b = y.down.type;
-        d.items_per_wave = ipw_env("DOWN", 2);
+        d.items_per_wave = ipw_env("DOWN", 1);
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
