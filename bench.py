@@ -24,6 +24,11 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch of the roofline kernel (layer gate/up matvec), from rocprofv3 FETCH_SIZE / WRITE_SIZE
+# passes over `bench.py --probe-traffic`, FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a
+# 1 GiB device copy reads on the same counters). Summary and commands: profiles/hbm_traffic_matvec_qwen3_8b_q4km.md
+GATE_UP_TRAFFIC_BYTES = 58_700_000
+
 CFG = dict(qwen3=True, hidden=4096, layers=36, q_heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=151936,
            rope_base=1e6, rms_eps=1e-6, weight_std=0.02, seed=0)
 
@@ -65,6 +70,41 @@ def cpu_baseline(path, info):
                       f"{secs:.1f} s single-threaded; tok/s = host GB/s / weight bytes per token"}
 
 
+def probe_traffic():
+    """Launch sequence measured by the FETCH_SIZE / WRITE_SIZE passes: 20 replays each of the layer-0 gate/up,
+    ffn_down and head matvecs (same kernels and shapes as the 36-layer model), then 5 copies of 1 GiB between
+    two device buffers (known bytes: 1 GiB read + 1 GiB written per dispatch) to scale the counters."""
+    import ribn_amd
+    cfg = dict(CFG, layers=1)
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_probe_{os.getpid()}.gguf")
+    ribn_amd.synth_qwen_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                             ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                             embd_type=ribn_amd.GGML_Q4_K, **cfg)
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=64, max_sequences=1) as m:
+            m.generate([1, 2, 3, 4], 2)
+            for which in (0, 1, 2):
+                ms, nbytes = m.bench_kernel(which, iters=20)
+                print(f"kernel {which}: {ms * 1e3:.2f} us, {nbytes} algorithmic bytes", flush=True)
+    finally:
+        os.unlink(path)
+    # the HIP runtime's own device-to-device blit kernel (no torch: its launches crash under counter collection)
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = 1 << 30
+    bufs = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for b in bufs:
+        assert hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(n)) == 0
+    assert hip.hipMemset(bufs[0], 1, ctypes.c_size_t(n)) == 0
+    for _ in range(5):
+        assert hip.hipMemcpy(bufs[1], bufs[0], ctypes.c_size_t(n), 3) == 0   # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    for b in bufs:
+        hip.hipFree(b)
+    print("copy: 5 x 1 GiB", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +114,9 @@ def main():
     ap.add_argument("--model", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
+    ap.add_argument("--probe-traffic", action="store_true",
+                    help="counter-collection workload for rocprofv3 --pmc: replays the gate/up, down and head "
+                         "launches of a 1-layer 8B-shape model, then a plain 1 GiB device copy as calibration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is designed, not built "
@@ -82,6 +125,9 @@ def main():
     import numpy as np
     import ribn_amd
 
+    if args.probe_traffic:
+        probe_traffic()
+        return
     cfg = dict(CFG)
     if args.layers:
         cfg["layers"] = args.layers
@@ -131,7 +177,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights, fp16-staged activations, fp32 accumulate, f16 KV",
+        "dtype": "q4_k/q6_k weights x int8 (two-level) staged activations, int32/fp32 accumulate, f16 KV",
         "data": "synthetic (seeded N(0,0.02) weights quantized to GGUF Q4_K_M; random prompt)",
         "config": {"workload": "qwen3-8b-shape Q4_K_M bs1 greedy decode (BASELINE configs[2])",
                    "prompt": args.prompt, "decode_tokens": args.steps, "layers": info.layers,
@@ -141,7 +187,8 @@ def main():
         "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+                     "traffic_unit": "bytes/launch",
                      "kernel": "matvec_kernel (layer-0 ffn gate/up, Q4_K 4096->2x12288, SwiGLU epilogue)",
                      "avg_us": round(kern_ms * 1e3, 2), "bytes_per_launch": int(kern_bytes)},
         "kernels_us": {"gate_up_q4k": round(kern_ms * 1e3, 2), "down_q6k": round(down_ms * 1e3, 2),

@@ -531,8 +531,8 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         set_err(err, err_len, arch + ".attention.head_count / head_count_kv must be an integer <= 8");
         return RIBN_ERR_FORMAT;
     }
-    if (M->H % 256 || M->F % 256 || M->H > 16384 || M->F > 28672) {
-        set_err(err, err_len, arch + ".embedding_length and feed_forward_length must be multiples of 256 "
+    if (M->H % 32 || M->F % 32 || M->H > 16384 || M->F > 28672) {
+        set_err(err, err_len, arch + ".embedding_length and feed_forward_length must be multiples of 32 "
                                      "(<= 16384 / 28672)");
         return RIBN_ERR_FORMAT;
     }
@@ -578,6 +578,13 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
                             ", " + std::to_string(rows) + "]",
                         RIBN_ERR_FORMAT);
         }
+        uint64_t be, bb;
+        type_layout(t->type, &be, &bb);
+        if (k % be)
+            return fail(nullptr, err, err_len,
+                        "tensor " + t->name + ": input length " + std::to_string(k) + " is not a multiple of the " +
+                            type_name(t->type) + " block (" + std::to_string(be) + ")",
+                        RIBN_ERR_FORMAT);
         HIPCHK(upload_qmat(M, t->type, rows, k, g.data(*t), q, staging));
         return RIBN_OK;
     };

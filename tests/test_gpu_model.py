@@ -1,7 +1,7 @@
 """GPU parity of the whole token loop and the executor contract.
 
 Bars (north star): per-layer hidden states and logits within rel-L2 2e-3 of the
-FP32 oracle (BF16 KV cache on the device), and identical greedy tokens for 64
+FP32 oracle (binary16 KV cache on the device, the reference's cache type), and identical greedy tokens for 64
 steps on seeded synthetic models. A greedy mismatch is excused only as a
 near-tie: the oracle's own logits must put the device's pick within the
 measured logit error of the oracle's pick; the run then stops comparing
@@ -31,6 +31,10 @@ MODELS = {
                                 vocab=1024, **Q4KM),
     "qwen2_q8_0_g7": dict(qwen3=False, hidden=448 + 64, layers=2, q_heads=14, kv_heads=2, head_dim=64, ffn=1024,
                           vocab=640, weight_type=ribn_amd.GGML_Q8_0),
+    # Qwen2.5-0.5B geometry (hidden 896 = 28 Q8_0 blocks, 14/2 heads x 64,
+    # FFN 4864, q/k/v bias, all Q8_0), at 2 layers and a reduced vocabulary
+    "qwen2_0p5b_shape_q8_0": dict(qwen3=False, hidden=896, layers=2, q_heads=14, kv_heads=2, head_dim=64,
+                                  ffn=4864, vocab=1024, weight_type=ribn_amd.GGML_Q8_0),
     "qwen3_g8_tied": dict(qwen3=True, hidden=512, layers=1, q_heads=8, kv_heads=1, head_dim=64, ffn=512,
                           vocab=256, tied_output=True, **Q4KM),
 }
@@ -135,7 +139,7 @@ def _oracle_greedy(path, prompt, n_new, ctx, kv_round=0):
 
 
 @pytest.mark.parametrize("kv", list(KV_MODES))
-@pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen2_q8_0_g7"])
+@pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen2_q8_0_g7", "qwen2_0p5b_shape_q8_0"])
 def test_greedy_64_tokens(model_paths, name, kv):
     path = model_paths[name]
     kv_round, tol = KV_MODES[kv]
