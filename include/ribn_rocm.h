@@ -61,6 +61,10 @@ typedef struct {
 /* KV cache in bfloat16 instead of the default binary16 (binary16 is the reference
  * CUDA cache type, kv_append_f16 nvidia/src/model_ops.rs:1258-1276). */
 #define RIBN_LOAD_KV_BF16 1u
+/* Run each token step as the chain of per-stage kernel launches (HIP graphs)
+ * instead of the persistent one-launch step kernel. The persistent kernel is
+ * used by default when one is compiled for the model's configuration. */
+#define RIBN_LOAD_LAUNCH_CHAIN 2u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);
@@ -79,6 +83,8 @@ typedef struct {
     uint64_t weight_bytes;     /* encoded bytes of all matrices on device */
     uint64_t kv_bytes;         /* KV pool bytes */
     uint32_t kv_f16;           /* 1: binary16 KV cache, 0: bfloat16 */
+    uint32_t persistent_step;  /* 1: token steps run as one persistent kernel launch */
+    uint32_t step_workgroups;  /* its grid size (co-resident workgroups) */
 } ribn_rocm_info_t;
 int ribn_rocm_info(const ribn_rocm_model *model, ribn_rocm_info_t *out);
 
@@ -189,6 +195,16 @@ int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, 
  * one launch streams (0 for attention). */
 int ribn_rocm_bench_model_kernel(ribn_rocm_model *model, uint32_t which, uint32_t iters, double *avg_ms,
                                  uint64_t *bytes, char *err, size_t err_len);
+
+/* Per-stage timing of one persistent decode step (no reference counterpart:
+ * a profiling aid). Runs one step of the scratch sequence at context `ctx`
+ * (the sequence must hold ctx positions, e.g. after ribn_rocm_generate) and
+ * writes workgroup 0's wall clock in ns from the step's start: at the start,
+ * after each of the 5 stages of every layer (QKV, attention, O, gate/up,
+ * down) and after the head; *n = 2 + 5 * layers. RIBN_ERR_INVALID if the model
+ * runs the launch chain. */
+int ribn_rocm_step_stamps(ribn_rocm_model *model, uint32_t ctx, double *out_ns, size_t cap, size_t *n,
+                          char *err, size_t err_len);
 
 /* ------------------------------------------------------------------------ */
 /* Synthetic model writer (test and benchmark inputs; no reference counterpart:

@@ -32,6 +32,7 @@ BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (25
 
 RIBN_OK, RIBN_PENDING = 0, 1
 LOAD_KV_BF16 = 1
+LOAD_LAUNCH_CHAIN = 2
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -71,7 +72,8 @@ class Info(ctypes.Structure):
                 ("layers", ctypes.c_uint32), ("q_heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
                 ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
                 ("rope_dims", ctypes.c_uint32), ("weight_bytes", ctypes.c_uint64), ("kv_bytes", ctypes.c_uint64),
-                ("kv_f16", ctypes.c_uint32)]
+                ("kv_f16", ctypes.c_uint32), ("persistent_step", ctypes.c_uint32),
+                ("step_workgroups", ctypes.c_uint32)]
 
 
 class TokenOptions(ctypes.Structure):
@@ -137,6 +139,8 @@ _sig("ribn_rocm_bench_gemv", _c.c_int, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c
 _sig("ribn_rocm_argmax", _c.c_int, _f32p, _c.c_uint64, _u32p, _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_bench_model_kernel", _c.c_int, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.POINTER(_c.c_double),
      _c.POINTER(_c.c_uint64), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_step_stamps", _c.c_int, _c.c_void_p, _c.c_uint32, _c.POINTER(_c.c_double), _c.c_size_t,
+     _c.POINTER(_c.c_size_t), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_synth_qwen_gguf", _c.c_int, _c.c_char_p, _c.POINTER(SynthConfig), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_quantize", _c.c_int, _c.c_uint32, _f32p, _c.c_uint64, _u8p)
 
@@ -259,9 +263,13 @@ class QwenRocm:
     """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
-                 kv_pages: int = 0, device: int = 0, kv: str = "f16"):
+                 kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain"):
+        """step: "persistent" (one kernel launch per token step when the library has a kernel compiled for
+        this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs)."""
+        if step not in ("persistent", "chain"):
+            raise ValueError("step must be 'persistent' or 'chain'")
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
-                           LOAD_KV_BF16 if kv == "bf16" else 0)
+                           (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_LAUNCH_CHAIN if step == "chain" else 0))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()
@@ -350,6 +358,14 @@ class QwenRocm:
         self._call(_lib.ribn_rocm_trace, _ptr(t, _u32p), n, _ptr(am, _u32p),
                    None if lg is None else _ptr(lg, _f32p), None if hd is None else _ptr(hd, _f32p))
         return am, lg, hd
+
+    def step_stamps(self, ctx: int):
+        """Per-stage wall-clock stamps (ns) of one persistent step at context ctx (see ribn_rocm_step_stamps)."""
+        cap = 2 + 5 * self.info.layers
+        out = (ctypes.c_double * cap)()
+        n = ctypes.c_size_t()
+        self._call(_lib.ribn_rocm_step_stamps, ctx, out, cap, ctypes.byref(n))
+        return np.frombuffer(out, dtype=np.float64, count=n.value).copy()
 
     def bench_kernel(self, which: int, iters: int = 50, ctx: int = 0):
         ms = ctypes.c_double()

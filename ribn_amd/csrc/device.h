@@ -1,0 +1,903 @@
+// Device code shared by the standalone kernels (kernels.hip) and the persistent
+// decode step (step.hip): value-type units, input staging, the matvec ring,
+// the decode-attention work item and the cross-workgroup hand-off helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include "kernels.h"
+
+namespace ribn {
+namespace {
+
+typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ u4_t ld_nt16(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
+}
+__device__ __forceinline__ u4_t ld16(const uint8_t* p) { return *reinterpret_cast<const u4_t*>(p); }
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}
+__device__ __forceinline__ uint32_t byte_at(uint32_t v, uint32_t j) { return (v >> (8u * j)) & 0xffu; }
+__device__ __forceinline__ uint32_t dword_at(const u4_t& v, uint32_t i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+// KV cache element encode (bf16 RNE, or binary16 RNE like kv_append_f16, model_ops.rs:1210-1276).
+__device__ __forceinline__ uint16_t kv_encode(float f, int f16) {
+    return f16 ? __half_as_ushort(__float2half_rn(f)) : f32_to_bf16(f);
+}
+template <bool F16>
+__device__ __forceinline__ float kv_decode(uint32_t b) {
+    if constexpr (F16) return __half2float(__ushort_as_half((unsigned short)b));
+    else return bf16_to_f32(b);
+}
+
+// Monotone key of model_ops.rs:193-199 packed with the inverted index, so
+// the u64 maximum is the largest logit with the lowest index. NaN -> 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    if (v != v) return 0ull;
+    uint32_t bits = __float_as_uint(v);
+    uint32_t key = (bits >> 31) ? ~bits : (bits ^ 0x80000000u);
+    return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+// Cross-workgroup hand-off inside one kernel. The eight XCD-local L2 caches are
+// not coherent with each other and an agent-scope fence writes back or
+// invalidates a whole L2 (buffer_wbl2 / buffer_inv), which costs tens of
+// microseconds across a grid. Instead, handed-off values move with agent-scope
+// atomic stores and loads (coherent per access), each wave waits until its
+// stores are acknowledged before its workgroup's arrival is counted, and the
+// arrival counter is a device-scope atomic.
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Count this workgroup's arrival; true in the last of `total` workgroups,
+// which also rearms the counter for the next launch.
+__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t total) {
+    __shared__ int last;
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = atomicAdd(ctr, 1u);
+        last = old == total - 1;
+        if (last) st_agent(ctr, 0u);
+    }
+    __syncthreads();
+    return last != 0;
+}
+
+// ---------------------------------------------------------------------------
+// Exact dequantization of one element, bit-identical to dequantize_block
+// (gguf/src/lib.rs:577-649): separate roundings, no contraction.
+__device__ __forceinline__ float canon_f16(uint32_t bits) {
+    float v = h2f(bits);
+    return (v != v) ? __uint_as_float(0x7fc00000u) : v;   // f16_to_f32: any NaN -> f32::NAN
+}
+
+__device__ float deq_elem(const QMat& w, uint32_t row, uint32_t e) {
+    const size_t nb = w.nb;
+    uint32_t blk = e / (w.type == 8 ? 32u : 256u);
+    uint32_t i = e % (w.type == 8 ? 32u : 256u);
+    size_t bi = (size_t)row * nb + blk;
+    if (w.type == 8) {
+        float d = canon_f16(*reinterpret_cast<const uint16_t*>(w.b + bi * 2));
+        int8_t q = (int8_t)w.a[bi * 32 + i];
+        return __fmul_rn(d, (float)q);
+    }
+    if (w.type == 12) {
+        // planes: a = qs, b = unpacked scales (dword p = sc(2p), sc(2p+1), m(2p), m(2p+1)), c = d | dmin
+        const uint8_t* dd = w.c + bi * 4;
+        float d = canon_f16(dd[0] | (dd[1] << 8)), dmin = canon_f16(dd[2] | (dd[3] << 8));
+        uint32_t g = i / 32, j = i % 32;
+        const uint8_t* sp = w.b + bi * 16 + (g / 2) * 4;
+        uint32_t sc = sp[g % 2], mn = sp[2 + g % 2];
+        uint32_t q = (w.a[bi * 128 + (g / 2) * 32 + j] >> ((g % 2) * 4)) & 15u;
+        float gs = __fmul_rn(d, (float)sc), gm = __fmul_rn(dmin, (float)mn);
+        return __fsub_rn(__fmul_rn(gs, (float)q), gm);
+    }
+    // Q6_K: scale s of sub-block s is at byte 2c + slot, c = 4(s/8) + s%4, slot = (s/4)%2
+    uint32_t g = i / 32, pos = i % 32, chunk = g / 4, variant = g % 4;
+    uint32_t lo = (w.a[bi * 128 + chunk * 64 + (variant % 2) * 32 + pos] >> (variant < 2 ? 0 : 4)) & 15u;
+    uint32_t hi = (w.b[bi * 64 + chunk * 32 + pos] >> (2 * variant)) & 3u;
+    float d = canon_f16(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
+    const uint32_t sidx = g * 2 + pos / 16;
+    int8_t sc = (int8_t)w.c[bi * 16 + 2 * (4 * (sidx / 8) + sidx % 4) + (sidx / 4) % 2];
+    float gs = __fmul_rn(d, (float)sc);
+    return __fmul_rn(gs, (float)((int)(lo | (hi << 4)) - 32));
+}
+
+// ---------------------------------------------------------------------------
+// Matvec input staging. x (optionally the RMSNorm input: rms_norm model_ops.rs:108,
+// x * (1/sqrt(sum/n + eps)) * w) is cut into groups of 16 values; each group gets
+// an fp32 scale s = max|v|/127 and two int8 parts, v ~ s (hi + lo/256), i.e.
+// about 15 significant bits, and the fp32 sum X of its values (for the Q4_K
+// minima and the Q6_K offset). The products with the quants then run on
+// v_dot4_i32_i8 with exact int32 accumulation. For an RMSNorm input the group
+// holds x*w and the normalisation factor 1/sqrt(mean(x^2)+eps) is returned as
+// an output multiplier, so x is read once.
+//
+// LDS layout: [k] int8 parts in unit planes | [k/16] (s, X) pairs | 64 fp32
+// reduction slots. Unit planes: plane j (Q4_K/Q6_K: 0..3, Q8_0: 0..1) holds,
+// for every unit u of the value type, the 16 bytes that unit's lane reads j-th
+// (hi then lo of its first 16 values, then hi and lo of its second 16), so
+// lane i of a wave reads the i-th 16 bytes of a plane (no bank conflicts).
+__host__ __device__ constexpr size_t mv_red_offset(int k) {
+    return ((size_t)k * 2 + (size_t)(k / 16) * 8 + 15) / 16 * 16;
+}
+
+// Unit, first plane (hi part; lo part in the next plane) and scale slot of the
+// 16 values x[16g .. 16g+16).
+template <int T>
+__device__ __forceinline__ void plane_of_group(int g, int& unit, int& plane, int& slot) {
+    if constexpr (T == 8) {
+        unit = g; plane = 0; slot = 0;
+    } else if constexpr (T == 12) {
+        const int blk = g >> 4, o = (g & 15) * 16, grp = o >> 5, hf = (o & 31) >> 4;
+        unit = blk * 8 + (grp >> 1) * 2 + hf;
+        plane = (grp & 1) * 2;
+        slot = grp & 1;
+    } else {
+        const int blk = g >> 4, o = (g & 15) * 16, chunk = o >> 7, v = (o & 127) >> 5, hf = (o & 31) >> 4;
+        unit = blk * 8 + chunk * 4 + (v & 1) * 2 + hf;
+        plane = (v >> 1) * 2;
+        slot = v >> 1;
+    }
+}
+
+template <int T>
+__device__ float stage_x(const MvArgs& a, int8_t* xs, float* gs, float* red) {
+    const int k = a.k, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+    const bool norm = a.norm_w != nullptr;
+    const int n_units = T == 8 ? k / 16 : k / 32;
+    u4_t* planes = reinterpret_cast<u4_t*>(xs);
+    float ss = 0.f;
+    for (int g = tid; g < k / 16; g += kThreads) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float4 t = x4[g * 4 + j];
+            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+            if (norm) {
+                const float4 w = w4[g * 4 + j];
+                t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
+            }
+            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        }
+        float am = 0.f, sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            am = fmaxf(am, fabsf(v[j]));
+            sum += v[j];
+        }
+        const float sc = am * (1.0f / 127.0f);
+        const float is = am > 0.f ? 127.0f / am : 0.f;
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t h4 = 0, l4 = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float vv = v[4 * j + b];
+                const float hq = rintf(vv * is);
+                const float lq = fminf(fmaxf(rintf((vv - hq * sc) * is * 256.0f), -127.f), 127.f);
+                h4 |= ((uint32_t)(int32_t)hq & 0xffu) << (8 * b);
+                l4 |= ((uint32_t)(int32_t)lq & 0xffu) << (8 * b);
+            }
+            hw[j] = h4;
+            lw[j] = l4;
+        }
+        int unit, plane, slot;
+        plane_of_group<T>(g, unit, plane, slot);
+        planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
+        planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
+        if constexpr (T == 8) {
+            gs[unit * 2] = sc;
+            gs[unit * 2 + 1] = sum;
+        } else {
+            gs[unit * 4 + slot] = sc;
+            gs[unit * 4 + 2 + slot] = sum;
+        }
+    }
+    float inv = 1.0f;
+    if (norm) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves; i++) ss += red[i];
+        inv = 1.0f / sqrtf(ss / (float)k + a.eps);
+    }
+    __syncthreads();
+    return inv;
+}
+
+// sum_j q_j x_j over 16 values for int8 bytes q (4 per dword) and x parts.
+__device__ __forceinline__ int dot16i(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& x) {
+    int acc = __builtin_amdgcn_sdot4((int)q0, (int)x.x, 0, false);
+    acc = __builtin_amdgcn_sdot4((int)q1, (int)x.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)q2, (int)x.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)q3, (int)x.w, acc, false);
+    return acc;
+}
+// s * sum_j q_j v_j for a group staged as v ~ s (hi + lo/256)
+__device__ __forceinline__ float dot16s(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& xh,
+                                        const u4_t& xl) {
+    const int h = dot16i(q0, q1, q2, q3, xh), l = dot16i(q0, q1, q2, q3, xl);
+    return fmaf((float)l, 1.0f / 256.0f, (float)h);
+}
+
+// ---------------------------------------------------------------------------
+// Per-lane work units. A unit is 16 bytes of quants of one row:
+//  Q4_K: 8 units per block; unit c holds nibble pairs of groups 2p, 2p+1 (p = c/2),
+//        elements 16*(c%2) .. +16 of each group (lib.rs:584-600 layout).
+//  Q6_K: 8 units per block; unit c holds ql bytes 16c..16c+15: low nibbles are
+//        group 4*(c/4) + (c/2)%2, high nibbles that group + 2 (lib.rs:623-649).
+//  Q8_0: 2 units per block (16 int8 each).
+// A wave walks 128 consecutive units of a row per load group (two halves of 64:
+// lane l takes units g0 + l and g0 + 64 + l), so every row offset is
+// wave-uniform and only the lane's fixed offset lives in a vector register.
+__device__ __forceinline__ uint32_t ld_nt32(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+__device__ __forceinline__ uint32_t ld_nt16b(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+}
+
+// base: wave-uniform pointer (scalar registers); off: the lane's 32-bit byte
+// offset, so the load uses scalar-base + vector-offset addressing.
+__device__ __forceinline__ u4_t ldo_nt16(const uint8_t* base, uint32_t off) { return ld_nt16(base + off); }
+
+template <int T>
+struct Unit;
+
+template <>
+struct Unit<12> {
+    static constexpr int kPerBlock = 8;
+    struct Raw { u4_t q; uint32_t s, dd; };
+    // unit u of `row`: quants, the lane's scale dword [sc(2p), sc(2p+1), m(2p), m(2p+1)], d|dmin
+    // units g0 + lane (g0 a multiple of 64, wave-uniform)
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        const size_t bi0 = row * w.nb + (size_t)(g0 >> 3);
+        const uint8_t* qa = w.a + (row * w.nb * 128 + (size_t)g0 * 16);
+        const uint8_t* sb = w.b + bi0 * 16;
+        const uint8_t* dc = w.c + bi0 * 4;
+        Raw r;
+        r.q = ld_nt16(qa + (uint32_t)(lane * 16));
+        r.s = ld_nt32(sb + (uint32_t)((lane >> 3) * 16 + ((lane & 7) >> 1) * 4));
+        r.dd = ld_nt32(dc + (uint32_t)((lane >> 3) * 4));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
+        const float4 G = reinterpret_cast<const float4*>(gs)[u];   // s_a, s_b, X_a, X_b
+        const uint32_t m = 0x0f0f0f0fu;
+        const float t0 = dot16s(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m, xs4[u], xs4[U + u]);
+        const float t1 = dot16s((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m, xs4[2 * U + u],
+                                xs4[3 * U + u]);
+        // sum_j x_j ((d sc) q_j - dmin m) = (d sc) s t - (dmin m) X, per group
+        acc = fmaf(d * (float)(r.s & 0xffu) * G.x, t0, acc);
+        acc = fmaf(-dmin * (float)((r.s >> 16) & 0xffu), G.z, acc);
+        acc = fmaf(d * (float)((r.s >> 8) & 0xffu) * G.y, t1, acc);
+        acc = fmaf(-dmin * (float)(r.s >> 24), G.w, acc);
+        return acc;
+    }
+};
+
+template <>
+struct Unit<14> {
+    static constexpr int kPerBlock = 8;
+    struct Raw { u4_t ql, qh; uint32_t sc, d; };
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        const size_t bi0 = row * w.nb + (size_t)(g0 >> 3);
+        const int c = lane & 7;
+        Raw r;
+        r.ql = ld_nt16(w.a + (row * w.nb * 128 + (size_t)g0 * 16) + (uint32_t)(lane * 16));
+        r.qh = ld_nt16(w.b + bi0 * 64 + (uint32_t)((lane >> 3) * 64 + 16 * (2 * (c >> 2) + (c & 1))));
+        r.sc = ld_nt16b(w.c + bi0 * 16 + (uint32_t)((lane >> 3) * 16 + 2 * c));
+        r.d = ld_nt16b(w.d + bi0 * 2 + (uint32_t)((lane >> 3) * 2));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const int vb = ((u & 7) >> 1) & 1;
+        const uint32_t s1 = 4 - 2 * vb, s2 = 2 * vb;
+        const uint32_t m4 = 0x0f0f0f0fu, m30 = 0x30303030u;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t l = dword_at(r.ql, i), h = dword_at(r.qh, i);
+            lo[i] = (l & m4) | ((h << s1) & m30);
+            hi[i] = ((l >> 4) & m4) | ((h >> s2) & m30);
+        }
+        const float d = h2f(r.d);
+        const float scl = (float)(int8_t)(r.sc & 0xffu), sch = (float)(int8_t)(r.sc >> 8);
+        const float4 G = reinterpret_cast<const float4*>(gs)[u];
+        const float t0 = dot16s(lo[0], lo[1], lo[2], lo[3], xs4[u], xs4[U + u]);
+        const float t1 = dot16s(hi[0], hi[1], hi[2], hi[3], xs4[2 * U + u], xs4[3 * U + u]);
+        // sum_j x_j (d sc)(q_j - 32) = (d sc)(s t - 32 X), per 16-value sub-block
+        acc = fmaf(d * scl, fmaf(G.x, t0, -32.0f * G.z), acc);
+        acc = fmaf(d * sch, fmaf(G.y, t1, -32.0f * G.w), acc);
+        return acc;
+    }
+};
+
+template <>
+struct Unit<8> {
+    static constexpr int kPerBlock = 2;
+    struct Raw { u4_t q; uint32_t d; };
+    static __device__ __forceinline__ Raw load_full(const QMat& w, size_t row, int g0, int lane) {
+        Raw r;
+        r.q = ld_nt16(w.a + (row * w.nb * 32 + (size_t)g0 * 16) + (uint32_t)(lane * 16));
+        r.d = ld_nt16b(w.b + (row * w.nb + (size_t)(g0 >> 1)) * 2 + (uint32_t)((lane >> 1) * 2));
+        return r;
+    }
+    static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
+        const float2 G = reinterpret_cast<const float2*>(gs)[u];
+        const float t = dot16s(r.q.x, r.q.y, r.q.z, r.q.w, xs4[u], xs4[U + u]);
+        return fmaf(h2f(r.d) * G.x, t, acc);
+    }
+};
+
+// A load group: two units of each of the two rows of an item, per lane.
+template <int T>
+struct Group {
+    typename Unit<T>::Raw a0, b0, a1, b1;
+};
+
+// Where a wave's work lives: items (two rows each, or one gate/up pair) of one
+// segment, walked as a flat sequence of load groups. Every field is wave-uniform.
+struct WaveWork {
+    const QMat* wa;
+    const QMat* wb;        // second row's matrix (the up matrix for gate/up pairs)
+    int first_item, n_items, n_rows, ngr, n_units;
+    bool pair;
+};
+
+// Loads of one group: wave-uniform row/group base (scalar registers) plus the
+// lane's 32-bit offset. Lanes past the end of a row (the last group of a row
+// whose unit count is not a multiple of 128) load a valid unit of the same row
+// and are masked out in mv_body.
+template <int T>
+__device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int it, int gi) {
+    using U = Unit<T>;
+    const int item = w.first_item + it * kWaves;
+    const int ra = w.pair ? item : 2 * item;
+    const int rb = w.pair ? item : min(ra + 1, w.n_rows - 1);
+    const int lane = threadIdx.x & 63;
+    const int g0 = gi * 128, g1 = g0 + 64 < w.n_units ? g0 + 64 : 0;
+    const int l0 = g0 + lane < w.n_units ? lane : 0, l1 = g1 + lane < w.n_units ? lane : 0;
+    g.a0 = U::load_full(*w.wa, (size_t)ra, g0, l0);
+    g.b0 = U::load_full(*w.wb, (size_t)rb, g0, l0);
+    g.a1 = U::load_full(*w.wa, (size_t)ra, g1, l1);
+    g.b1 = U::load_full(*w.wb, (size_t)rb, g1, l1);
+}
+
+// Position (item, group) of a wave's walk, advanced one load group at a time.
+struct Cursor {
+    int it, gi;
+    __device__ __forceinline__ void next(int ngr) {
+        if (++gi == ngr) { gi = 0; ++it; }
+    }
+};
+
+// The wave's load groups live in a ring of P register slots: slot j is
+// computed, then refilled with the group P positions ahead, so P-1 groups of
+// 128-bit loads are in flight while one is computed. The first P groups are
+// issued before the workgroup waits for its input (mv_run).
+template <int T, int MODE, int P>
+__device__ __forceinline__ void mv_body(const MvSeg& sg, const WaveWork& w, Group<T> (&ring)[P], Cursor ld,
+                                        const u4_t* xs4, const float* gs, float oscale, uint64_t& best) {
+    using U = Unit<T>;
+    const int lane = threadIdx.x & 63;
+    const int total = w.n_items * w.ngr;
+    float a0 = 0.f, b0 = 0.f;
+    Cursor c{0, 0};
+    for (int q0 = 0; q0 < total; q0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            // one slot at a time: without this fence the scheduler interleaves
+            // the LDS reads of all P slots and the register demand multiplies
+            __builtin_amdgcn_sched_barrier(0);
+            if (q0 + j < total) {
+                const int u0 = c.gi * 128 + lane, u1 = u0 + 64;
+                if (u0 < w.n_units) {
+                    a0 = U::apply(ring[j].a0, u0, xs4, w.n_units, gs, a0);
+                    b0 = U::apply(ring[j].b0, u0, xs4, w.n_units, gs, b0);
+                }
+                if (u1 < w.n_units) {
+                    a0 = U::apply(ring[j].a1, u1, xs4, w.n_units, gs, a0);
+                    b0 = U::apply(ring[j].b1, u1, xs4, w.n_units, gs, b0);
+                }
+                if (q0 + j + P < total) {
+                    // keep the refill after the slot's last use: otherwise the
+                    // scheduler hoists it and holds two copies of every slot
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_group<T>(ring[j], w, ld.it, ld.gi);
+                    ld.next(w.ngr);
+                }
+                if (c.gi == w.ngr - 1) {
+                    float ya = wave_sum(a0) * oscale, yb = wave_sum(b0) * oscale;
+                    a0 = b0 = 0.f;
+                    const int item = w.first_item + c.it * kWaves;
+                    const int ra = w.pair ? item : 2 * item;
+                    const int rb = w.pair ? item : ra + 1;
+                    if (lane == 0) {
+                        const bool has_b = !w.pair && rb < w.n_rows;
+                        if (sg.bias) {
+                            ya += sg.bias[ra];
+                            if (has_b) yb += sg.bias[rb];
+                        }
+                        // outputs are written through to memory (agent-scope stores)
+                        // so workgroups on other XCDs read them after a grid barrier
+                        if constexpr (MODE == MV_ADD) {
+                            st_agent(sg.out + ra, sg.res[ra] + ya);
+                            if (has_b) st_agent(sg.out + rb, sg.res[rb] + yb);
+                        } else if constexpr (MODE == MV_SILU) {
+                            st_agent(sg.out + ra, ya / (1.0f + expf(-ya)) * yb);
+                        } else {
+                            st_agent(sg.out + ra, ya);
+                            if (has_b) st_agent(sg.out + rb, yb);
+                            if constexpr (MODE == MV_HEAD) {
+                                best = max(best, argmax_key(ya, (uint32_t)ra));
+                                if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
+                            }
+                        }
+                    }
+                }
+                c.next(w.ngr);
+            }
+        }
+    }
+}
+
+// Issue the first P load groups, wait for the input (sync: a grid barrier in
+// the persistent step, nothing in a standalone launch), stage it, run the ring.
+// Returns false if sync reports a failed barrier.
+template <int T, int MODE, int P, typename Sync>
+__device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWork& w, int8_t* xs, float* gs,
+                                       float* red, uint64_t& best, Sync&& sync) {
+    w.n_units = (int)sg.w.nb * Unit<T>::kPerBlock;
+    w.ngr = (w.n_units + 127) / 128;
+    const int total = w.n_items * w.ngr;
+    Group<T> ring[P];
+    Cursor ld{0, 0};
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        if (j < total) {
+            load_group<T>(ring[j], w, ld.it, ld.gi);
+            ld.next(w.ngr);
+        }
+    }
+    if (!sync()) return false;
+    const float oscale = stage_x<T>(a, xs, gs, red);
+    const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
+    mv_body<T, MODE, P>(sg, w, ring, ld, xs4, gs, oscale, best);
+    return true;
+}
+
+struct NoSync {
+    __device__ __forceinline__ bool operator()() const { return true; }
+};
+
+// One workgroup's share of a matvec launch laid out in `a` (segments, items per
+// wave). Workgroups beyond the layout only sync. LDS: staged input at `lds`.
+template <int TA, int TB, int MODE, int P, typename Sync>
+__device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uint64_t& best, Sync&& sync) {
+    int8_t* xs = reinterpret_cast<int8_t*>(lds);
+    float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
+    float* red = reinterpret_cast<float*>(lds + mv_red_offset(a.k));
+    int si = 0;
+    if (a.nseg > 1 && wg >= a.seg[1].wg_begin) si = 1;
+    if (a.nseg > 2 && wg >= a.seg[2].wg_begin) si = 2;
+    const MvSeg& sg = a.seg[si];
+    const int lwg = wg - sg.wg_begin;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr bool pair = MODE == MV_SILU;
+    WaveWork w;
+    w.wa = &sg.w;
+    w.wb = pair ? &sg.w2 : &sg.w;
+    w.pair = pair;
+    w.n_rows = (int)sg.w.rows;
+    w.first_item = lwg * sg.ipw * kWaves + wave;
+    const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
+    w.n_items = max(0, min(sg.ipw, (n_item_total - w.first_item + kWaves - 1) / kWaves));
+    if (si == 2 && TB != TA) return mv_run<TB, MODE, P>(a, sg, w, xs, gs, red, best, sync);
+    return mv_run<TA, MODE, P>(a, sg, w, xs, gs, red, best, sync);
+}
+
+// Greedy token of the head launch: first maximum over the vocabulary, NaN
+// skipped (model_ops.rs:203-260). Every one of the n_wg workgroups publishes its
+// best key; the last to arrive reduces them and writes the token into the
+// active sequence (tokens[pos + 1], position advanced).
+__device__ __forceinline__ void head_finish(const MvArgs& a, uint64_t best, int wg, int n_wg) {
+    __shared__ uint64_t wbest[kWaves];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) best = max(best, (uint64_t)__shfl_xor(best, o));
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = wbest[0];
+        for (int i = 1; i < kWaves; i++) b = max(b, wbest[i]);
+        st_agent(a.head.partial + wg, b);
+    }
+    if (arrive_last(a.head.counter, n_wg)) {
+        uint64_t b = 0ull;
+        for (int i = threadIdx.x; i < n_wg; i += kThreads) b = max(b, ld_agent(a.head.partial + i));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
+        __syncthreads();
+        if (lane == 0) wbest[wave] = b;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            b = wbest[0];
+            for (int i = 1; i < kWaves; i++) b = max(b, wbest[i]);
+            const uint32_t tok = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
+            SeqState* s = a.ctl->seq;
+            const int pos = s->pos;
+            if (pos + 1 <= s->max_ctx) s->tokens[pos + 1] = tok;
+            s->last_token = tok;
+            s->pos = pos + 1;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GQA decode attention over the paged KV cache with split-K over the context
+// (attn_score_gqa_paged, model_ops.rs:442-590; host equations
+// qwen_reference.rs:368-461, dense Qwen3: no gate). Workgroup (split, kv head);
+// the G = hq/hkv query heads of a KV head share every K/V load.
+//  * the split's K and V are staged in LDS in tiles of 64 positions (16-byte
+//    loads, the first tile issued before the prologue so its latency overlaps);
+//  * prologue: q (G heads) and k of the current token get per-head RMSNorm
+//    (qwen_reference.rs:382-400) and NeoX rope from the step table; the
+//    workgroup whose split holds the current position appends k, v
+//    (kv_append_f16, model_ops.rs:1258);
+//  * scores: 4 lanes per position, 1/4 of head_dim each, for all G heads;
+//  * exact softmax statistics of the split, then P.V over the V tiles;
+//  * splits are merged by log-sum-exp in the last workgroup of a KV head.
+// Every key and value, including the current token's, is used at the cache's
+// precision, as the reference reads its F16 cache.
+constexpr int kTile = 64;
+
+template <int HD, bool F16>
+struct KvTile {
+    static constexpr int kLoads = kTile * HD * 2 / 16 / kThreads;   // 16-byte loads per thread
+    u4_t r[kLoads];
+    // position i*kThreads/(HD/8)... : load index j -> (token, chunk)
+    __device__ __forceinline__ void load(const uint16_t* cache, const int* pg, int hkv, int kvh, int c0, int n,
+                                         int t0) {
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            const int idx = j * kThreads + threadIdx.x;
+            const int tl = c0 + idx / (HD / 8), ch = idx % (HD / 8);
+            if (tl < n) {
+                const int t = t0 + tl;
+                r[j] = *reinterpret_cast<const u4_t*>(
+                    cache + ((size_t)(pg[tl / kPageTokens] * hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD + ch * 8);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t (*tile)[HD]) const {
+#pragma unroll
+        for (int j = 0; j < kLoads; j++) {
+            const int idx = j * kThreads + threadIdx.x;
+            *reinterpret_cast<u4_t*>(&tile[idx / (HD / 8)][(idx % (HD / 8)) * 8]) = r[j];
+        }
+    }
+};
+
+template <int HD, int G>
+struct AttnLds {
+    static constexpr int NS = kThreads / (HD / 8);
+    float buf[G + 2][HD];                // q heads, k, v of the current token
+    uint16_t kt[kTile][HD];
+    uint16_t vt[kTile][HD];
+    float sc[G][kMaxSplitTokens];        // scores, then probabilities
+    float red[NS][HD];                   // P.V reduction
+    float stat[2][G];                    // per-head max, sum
+    int pg[kMaxSplitTokens / kPageTokens];
+};
+
+// One (split, KV head) work item. `pos` is the active position and `pages`
+// the sequence's page table. In a standalone launch the raw q/k/v loads go
+// first (they do not depend on the position); in the persistent step the first
+// K/V tile is fetched before `sync` (the barrier after the QKV projection), as
+// cached keys and values do not depend on this step, and q/k/v after it.
+// Returns false if sync reports a failed barrier.
+template <int HD, int G, bool F16, bool PERSIST, typename Sync>
+__device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, const int32_t* pages, uint8_t* lds_raw,
+                               Sync&& sync) {
+    constexpr int CH = HD / 8;                 // 16-byte chunks per row
+    constexpr int NS = kThreads / CH;          // token slices in P.V
+    constexpr int REC = G * HD + 2 * G;        // partial record floats
+    constexpr int DQ = HD / 4;                 // dims per lane in the scores
+    AttnLds<HD, G>& L = *reinterpret_cast<AttnLds<HD, G>*>(lds_raw);
+    auto& buf = L.buf;
+    auto& kt = L.kt;
+    auto& vt = L.vt;
+    auto& sc = L.sc;
+    auto& red = L.red;
+    auto& stat = L.stat;
+    auto& pg = L.pg;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int qd = a.hq * HD, kd = a.hkv * HD;
+    constexpr int NRAW = (G + 2 + (kThreads / HD) - 1) / (kThreads / HD);
+    float rawv[NRAW];   // q/k/v rows of this KV head
+    auto load_rawv = [&]() {
+#pragma unroll
+        for (int j = 0; j < NRAW; j++) {
+            const int i = j * kThreads + tid;
+            if (i < (G + 2) * HD) {
+                const int r = i / HD, d = i % HD;
+                const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
+                                         : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
+                rawv[j] = src[d];
+            }
+        }
+    };
+    if constexpr (!PERSIST) load_rawv();
+    const int ctx = pos + 1;
+    int per = (ctx + a.n_splits - 1) / a.n_splits;
+    per = (per + kPageTokens - 1) / kPageTokens * kPageTokens;
+    if (per > kMaxSplitTokens) {
+        // A split wider than the LDS tiles: too few splits for this context.
+        // Poison the output instead of touching memory.
+        if (split == 0)
+            for (int i = tid; i < G * HD; i += kThreads) st_agent(a.out + (size_t)kvh * G * HD + i, __uint_as_float(0x7fc00000u));
+        return sync();
+    }
+    const int t0 = split * per, t1 = min(ctx, t0 + per), n = max(0, t1 - t0);
+    const bool owner = t0 <= pos && pos < t1;
+
+    __syncthreads();   // LDS may still be in use by this workgroup's previous work item
+    for (int i = tid; i < n; i += kThreads)
+        if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = pages[(t0 + i) / kPageTokens];
+    __syncthreads();
+    KvTile<HD, F16> kpre, vpre;   // first tile in flight during the prologue
+    kpre.load(a.kcache, pg, a.hkv, kvh, 0, n, t0);
+    vpre.load(a.vcache, pg, a.hkv, kvh, 0, n, t0);
+    if (!sync()) return false;
+    if constexpr (PERSIST) load_rawv();
+#pragma unroll
+    for (int j = 0; j < NRAW; j++) {
+        const int i = j * kThreads + tid;
+        if (i < (G + 2) * HD) buf[i / HD][i % HD] = rawv[j];
+    }
+    __syncthreads();
+
+    // -- prologue: per-head norm, rope, current token at cache precision
+    if (a.q_norm) {
+        for (int r = wave; r <= G; r += kWaves) {
+            const float* nw = r < G ? a.q_norm : a.k_norm;
+            float ss = 0.f;
+            for (int d = lane; d < HD; d += 64) ss += buf[r][d] * buf[r][d];
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            for (int d = lane; d < HD; d += 64) buf[r][d] = buf[r][d] * inv * nw[d];
+        }
+        __syncthreads();
+    }
+    const int half = a.rot / 2;
+    for (int i = tid; i < (G + 1) * half; i += kThreads) {
+        const int r = i / half, p = i % half;
+        const float c = a.rope[p], sn = a.rope[half + p];
+        const float x0 = buf[r][p], x1 = buf[r][p + half];
+        buf[r][p] = x0 * c - x1 * sn;
+        buf[r][p + half] = x0 * sn + x1 * c;
+    }
+    __syncthreads();
+    uint16_t cur_e = 0;
+    if (tid < 2 * HD) {
+        const int r = G + tid / HD, d = tid % HD;
+        cur_e = kv_encode(buf[r][d], F16 ? 1 : 0);
+        if (owner) {
+            const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
+            uint16_t* dst = (r == G ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
+            dst[d] = cur_e;
+        }
+    }
+    // scale q into the log2 domain
+    for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
+    __syncthreads();
+
+    // -- scores, tile by tile: lane group of 4 per position
+    const int stl = tid >> 2, part = tid & 3;
+    for (int c0 = 0; c0 < n; c0 += kTile) {
+        if (c0 == 0) kpre.store(kt);
+        else {
+            KvTile<HD, F16> kk;
+            kk.load(a.kcache, pg, a.hkv, kvh, c0, n, t0);
+            kk.store(kt);
+        }
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
+            __syncthreads();
+            if (tid < HD) kt[pos - t0 - c0][tid] = cur_e;
+        }
+        __syncthreads();
+        const int tl = c0 + stl;
+        float acc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) acc[g] = 0.f;
+#pragma unroll
+        for (int c = 0; c < DQ / 8; c++) {
+            const int d0 = part * DQ + c * 8;
+            const u4_t kw = *reinterpret_cast<const u4_t*>(&kt[stl][d0]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = dword_at(kw, i);
+                const float k0 = kv_decode<F16>(w & 0xffffu), k1 = kv_decode<F16>(w >> 16);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float2 qq = *reinterpret_cast<const float2*>(&buf[g][d0 + 2 * i]);
+                    acc[g] = fmaf(qq.x, k0, acc[g]);
+                    acc[g] = fmaf(qq.y, k1, acc[g]);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            acc[g] += __shfl_xor(acc[g], 1);
+            acc[g] += __shfl_xor(acc[g], 2);
+        }
+        if (part == 0 && tl < n) {
+#pragma unroll
+            for (int g = 0; g < G; g++) sc[g][tl] = acc[g];
+        }
+        __syncthreads();
+    }
+
+    // -- softmax statistics per head
+    for (int g = wave; g < G; g += kWaves) {
+        float m = -INFINITY;
+        for (int tl = lane; tl < n; tl += 64) m = fmaxf(m, sc[g][tl]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int tl = lane; tl < n; tl += 64) {
+            const float p = exp2f(sc[g][tl] - m);
+            sc[g][tl] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) { stat[0][g] = m; stat[1][g] = l; }
+    }
+    __syncthreads();
+
+    // -- o[g] = sum_t p[g][t] v[t]
+    const int ch = tid % CH, sl = tid / CH;
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[g][i] = 0.f;
+    for (int c0 = 0; c0 < n; c0 += kTile) {
+        if (c0 > 0) __syncthreads();
+        if (c0 == 0) vpre.store(vt);
+        else {
+            KvTile<HD, F16> vv;
+            vv.load(a.vcache, pg, a.hkv, kvh, c0, n, t0);
+            vv.store(vt);
+        }
+        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
+            __syncthreads();
+            if (tid >= HD && tid < 2 * HD) vt[pos - t0 - c0][tid - HD] = cur_e;
+        }
+        __syncthreads();
+        const int lim = min(kTile, n - c0);
+        for (int j = sl; j < lim; j += NS) {
+            const u4_t vw = *reinterpret_cast<const u4_t*>(&vt[j][ch * 8]);
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = dword_at(vw, i);
+                v[2 * i] = kv_decode<F16>(w & 0xffffu);
+                v[2 * i + 1] = kv_decode<F16>(w >> 16);
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float p = sc[g][c0 + j];
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[g][i] = fmaf(p, v[i], o[g][i]);
+            }
+        }
+    }
+    const bool direct = a.n_splits == 1;
+    float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) red[sl][ch * 8 + i] = o[g][i];
+        __syncthreads();
+        if (tid < HD) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < NS; j++) acc += red[j][tid];
+            if (direct) st_agent(a.out + (size_t)(kvh * G + g) * HD + tid, acc / stat[1][g]);
+            else st_agent(rec + g * HD + tid, acc);
+        }
+        __syncthreads();
+    }
+    if (direct) return true;
+    if (tid < G) {
+        st_agent(rec + G * HD + tid, n > 0 ? stat[0][tid] : -INFINITY);
+        st_agent(rec + G * HD + G + tid, n > 0 ? stat[1][tid] : 0.f);
+    }
+    if (!arrive_last(a.counters + kvh, a.n_splits)) return true;
+
+    // -- merge the splits of this KV head (log-sum-exp in base 2). The split
+    //    statistics are fetched in one parallel batch, then each output
+    //    element's partials with all loads issued before any is used.
+    const float* base = a.part + (size_t)kvh * a.n_splits * REC;
+    float* smx = &sc[0][0];                        // [G][n_splits] maxima (scores are dead)
+    float* swt = &sc[0][0] + G * kMaxSplits;       // [G][n_splits] weights
+    for (int i = tid; i < G * a.n_splits; i += kThreads) {
+        const int g = i / a.n_splits, sp = i % a.n_splits;
+        smx[i] = ld_agent(base + (size_t)sp * REC + G * HD + g);
+        swt[i] = ld_agent(base + (size_t)sp * REC + G * HD + G + g);
+    }
+    __syncthreads();
+    if (tid < G) {
+        float mx = -INFINITY;
+        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, smx[tid * a.n_splits + sp]);
+        float lt = 0.f;
+        for (int sp = 0; sp < a.n_splits; sp++) {
+            const float ms = smx[tid * a.n_splits + sp];
+            const float wgt = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+            lt += swt[tid * a.n_splits + sp] * wgt;
+            swt[tid * a.n_splits + sp] = wgt;
+        }
+        stat[1][tid] = lt;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD;
+        const float* w8 = swt + g * a.n_splits;
+        float acc = 0.f;
+        for (int sp0 = 0; sp0 < a.n_splits; sp0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                v[j] = sp0 + j < a.n_splits ? ld_agent(base + (size_t)(sp0 + j) * REC + idx) : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (sp0 + j < a.n_splits) acc = fmaf(v[j], w8[sp0 + j], acc);
+        }
+        st_agent(a.out + (size_t)kvh * G * HD + idx, acc / stat[1][g]);
+    }
+    return true;
+}
+
+}  // namespace
+}  // namespace ribn

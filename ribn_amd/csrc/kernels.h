@@ -10,6 +10,16 @@ constexpr int kPageTokens = 16;   // KV page size (crates/qwen/src/gguf.rs:16)
 constexpr int kMaxSplits = 128;   // split-K limit of decode attention
 constexpr int kMaxSplitTokens = 512;   // positions one attention workgroup covers
 
+// Decode-attention splits for a context of `ctx` positions: about 64 positions
+// per workgroup, a power of two, at most kMaxSplits (a split then covers at
+// most kMaxSplitTokens positions for contexts up to kMaxSplits * kMaxSplitTokens).
+__host__ __device__ inline int splits_for_ctx(int ctx) {
+    const int want = (ctx + 63) / 64;
+    int s = 1;
+    while (s < want && s < kMaxSplits) s <<= 1;
+    return s;
+}
+
 // A quantized matrix after load-time re-tiling: `rows` output rows of `k`
 // inputs, GGML row n = input-contiguous. Each GGML block is split into
 // 16-byte-aligned planes so every wavefront load is a coalesced 128-bit load:
@@ -69,9 +79,10 @@ struct MvSeg {
     QMat w;
     QMat w2;             // MV_SILU: the up matrix (same type/shape as w)
     float* out;
+    const float* res;    // MV_ADD: residual input, out[row] = res[row] + y (res == out: in place)
     const float* bias;   // optional per-row bias
     int32_t wg_begin;    // first workgroup of this segment
-    int32_t pad;
+    int32_t ipw;         // items per wave in this segment
 };
 
 struct HeadEpi {
@@ -88,7 +99,7 @@ struct MvArgs {
     int32_t k;
     int32_t mode;
     int32_t nseg;
-    int32_t items_per_wave;  // item = 2 weight rows (or one gate/up pair)
+    int32_t items_per_wave;  // default items per wave (item = 2 weight rows, or one gate/up pair)
     uint32_t type_a, type_b;
     MvSeg seg[3];
     HeadEpi head;
@@ -123,6 +134,33 @@ struct AttnArgs {
     float scale_log2;        // log2(e) / sqrt(hd)
 };
 
+// Persistent decode step: one launch runs a whole token step (embedding, every
+// layer, head) with grid-wide barriers between dependent stages. Every stage
+// writes a buffer of its own in a per-step arena, so no buffer is written after
+// any workgroup has read it within a launch.
+struct LayerDev {
+    MvArgs qkv, o, gu, down;   // laid out for the persistent grid
+    AttnArgs attn;             // n_splits is chosen in the kernel from the context
+};
+
+// Bytes of the persistent step's barrier state: 18 words spaced 64 words
+// (256 bytes) apart, rounded up (layout in step.h).
+constexpr int kStepBarWords = 64 * 18;
+constexpr size_t kStepBarBytes = 8192;
+static_assert(kStepBarWords * 4 <= (int)kStepBarBytes, "barrier state larger than its allocation");
+
+struct StepArgs {
+    const LayerDev* layers;
+    int32_t n_layers;
+    int32_t head;              // 1: final norm + head + argmax; 0: advance the position only
+    EmbedArgs embed;           // embed.h = arena h0
+    MvArgs head_mv;
+    uint32_t* bar;             // grid barrier state: kStepBarBytes, zeroed at load (layout in step.h)
+    uint64_t timeout_ticks;    // barrier wait limit in wall-clock ticks
+    const StepCtl* ctl;
+    uint64_t* stamps;          // optional: workgroup 0's wall clock at start and after each stage
+};
+
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);
 int matvec_rows_per_wg(const MvArgs& a);
@@ -131,6 +169,16 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t stream);
 hipError_t launch_dequant(const QMat& w, float* out, hipStream_t stream);
+// A compiled configuration of the persistent step kernel: matrix value types
+// (q/k, v, attn_output, gate/up, down, head), head dimension, query heads per
+// KV head, KV element type.
+struct StepKey {
+    int qa, qb, o, gu, dn, ht, hd, g, kv_f16;
+};
+// Workgroups of the step kernel for `key` that fit on the device at once (0:
+// no compiled kernel for this configuration); *lds receives its LDS bytes.
+int step_grid(const StepKey& key, int max_k, int device, size_t* lds);
+hipError_t launch_step(const StepArgs& a, const StepKey& key, int n_wg, size_t lds, hipStream_t stream);
 hipError_t launch_argmax(const float* logits, uint32_t n, uint64_t* partial, uint32_t* counter,
                          uint32_t* out, hipStream_t stream);
 

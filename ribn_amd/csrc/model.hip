@@ -50,15 +50,6 @@ struct Submission {
     hipEvent_t done = nullptr;
 };
 
-// Decode-attention splits: about 64 positions per workgroup, a power of two
-// (one graph per bucket), at most kMaxSplits; a split then covers at most
-// kMaxSplitTokens positions for every context the loader admits.
-int splits_for_ctx(int ctx) {
-    const int want = (ctx + 63) / 64;
-    int s = 1;
-    while (s < want && s < kMaxSplits) s <<= 1;
-    return s;
-}
 
 std::string hip_msg(const char* what, hipError_t e) {
     return std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
@@ -110,6 +101,16 @@ struct ribn_rocm_model {
     std::vector<int> wg_qkv, wg_o, wg_gu, wg_down;
     MvArgs mv_head{};
     std::map<int, hipGraphExec_t> graphs;   // key: n_splits * 2 + head
+
+    // persistent step (one launch per token); step_wg == 0: launch chain only
+    int step_wg = 0;
+    size_t step_lds = 0;
+    StepKey step_key{};
+    StepArgs step_args{};
+    LayerDev* d_layers = nullptr;
+    uint32_t* step_bar = nullptr;
+    float* arena_h0 = nullptr;
+    std::vector<float*> arena_h2;   // residual stream after each layer
 
     // executor state
     std::map<uint64_t, Sequence> seqs;
@@ -281,9 +282,56 @@ int layout_segments(MvArgs& a) {
     const int rpw = matvec_rows_per_wg(a);
     int wg = 0;
     for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].ipw = a.items_per_wave;
+        if (!a.seg[i].res) a.seg[i].res = a.seg[i].out;   // standalone launches add in place
         a.seg[i].wg_begin = wg;
         wg += ((int)a.seg[i].w.rows + rpw - 1) / rpw;
     }
+    return wg;
+}
+
+// Lay a launch out on a fixed grid of n_wg workgroups (the persistent step):
+// each segment gets ceil(items / (4 ipw)) workgroups; items per wave start at 1
+// and grow, one segment at a time where the longest per-wave work grows least,
+// until the segments fit. Returns the workgroups used (<= n_wg).
+int layout_grid(MvArgs& a, int n_wg) {
+    const bool pair = a.mode == MV_SILU;
+    int items[3] = {0, 0, 0}, ipw[3] = {1, 1, 1}, wgs[3] = {0, 0, 0};
+    double item_bytes[3] = {0, 0, 0};
+    for (int i = 0; i < a.nseg; i++) {
+        const QMat& w = a.seg[i].w;
+        uint64_t be, bb;
+        type_layout(w.type, &be, &bb);
+        items[i] = pair ? (int)w.rows : ((int)w.rows + 1) / 2;
+        item_bytes[i] = 2.0 * (double)w.k / (double)be * (double)bb;
+    }
+    auto total = [&]() {
+        int t = 0;
+        for (int i = 0; i < a.nseg; i++) {
+            wgs[i] = (items[i] + 4 * ipw[i] - 1) / (4 * ipw[i]);
+            t += wgs[i];
+        }
+        return t;
+    };
+    while (total() > n_wg) {
+        int best = -1;
+        double best_cost = 0;
+        for (int i = 0; i < a.nseg; i++) {
+            if (wgs[i] <= 1) continue;
+            const double cost = (ipw[i] + 1) * item_bytes[i];
+            if (best < 0 || cost < best_cost) { best = i; best_cost = cost; }
+        }
+        if (best < 0) break;
+        ipw[best]++;
+    }
+    int wg = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].ipw = ipw[i];
+        if (!a.seg[i].res) a.seg[i].res = a.seg[i].out;
+        a.seg[i].wg_begin = wg;
+        wg += wgs[i];
+    }
+    a.items_per_wave = ipw[0];
     return wg;
 }
 
@@ -368,6 +416,99 @@ AttnArgs attn_args(ribn_rocm_model* M, int l, int n_splits) {
     return at;
 }
 
+size_t align_floats(size_t n) { return (n + 63) / 64 * 64; }   // 256-byte sub-buffers
+
+// Persistent-step configuration: a compiled kernel must exist for the model's
+// value types, head dimension, query heads per KV head and KV element type,
+// with every layer using the same types. Activations go to a per-step arena
+// where every stage has its own buffer (see step.h).
+hipError_t build_step(ribn_rocm_model* M, bool allow) {
+    M->step_wg = 0;
+    if (!allow) return hipSuccess;
+    const Layer& y0 = M->layers[0];
+    StepKey key{(int)y0.q.type, (int)y0.v.type, (int)y0.o.type, (int)y0.gate.type, (int)y0.down.type,
+                (int)M->out.type, M->hd, M->hq / M->hkv, M->kv_f16 ? 1 : 0};
+    for (const Layer& y : M->layers)
+        if ((int)y.q.type != key.qa || (int)y.v.type != key.qb || (int)y.o.type != key.o ||
+            (int)y.gate.type != key.gu || (int)y.down.type != key.dn)
+            return hipSuccess;
+    size_t lds = 0;
+    const int max_k = std::max(std::max(M->H, M->F), M->hq * M->hd);
+    const int n_wg = step_grid(key, max_k, M->device, &lds);
+    if (n_wg < 64) return hipSuccess;
+
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    const size_t s_raw = align_floats(qd + 2 * kd), s_attn = align_floats(qd), s_h = align_floats(M->H),
+                 s_act = align_floats(M->F);
+    const size_t per_layer = s_raw + s_attn + 2 * s_h + s_act;
+    float* arena = nullptr;
+    hipError_t e = dalloc(M, &arena, sizeof(float) * (s_h + per_layer * M->L));
+    if (e != hipSuccess) return e;
+    M->arena_h0 = arena;
+    M->arena_h2.assign(M->L, nullptr);
+    std::vector<LayerDev> ld(M->L);
+    const float* prev = M->arena_h0;
+    for (int l = 0; l < M->L; l++) {
+        float* base = arena + s_h + per_layer * l;
+        float *raw = base, *att = raw + s_raw, *h1 = att + s_attn, *act = h1 + s_h, *h2 = act + s_act;
+        LayerDev& L = ld[l];
+        L.qkv = M->mv_qkv[l];
+        L.qkv.x = prev;
+        L.qkv.seg[0].out = raw; L.qkv.seg[1].out = raw + qd; L.qkv.seg[2].out = raw + qd + kd;
+        for (auto& sg : L.qkv.seg) sg.res = nullptr;
+        layout_grid(L.qkv, n_wg);
+        L.attn = attn_args(M, l, 1);
+        L.attn.raw = raw;
+        L.attn.out = att;
+        L.o = M->mv_o[l];
+        L.o.x = att;
+        L.o.seg[0].out = h1;
+        L.o.seg[0].res = prev;
+        layout_grid(L.o, n_wg);
+        L.gu = M->mv_gu[l];
+        L.gu.x = h1;
+        L.gu.seg[0].out = act;
+        L.gu.seg[0].res = nullptr;
+        layout_grid(L.gu, n_wg);
+        L.down = M->mv_down[l];
+        L.down.x = act;
+        L.down.seg[0].out = h2;
+        L.down.seg[0].res = h1;
+        layout_grid(L.down, n_wg);
+        M->arena_h2[l] = h2;
+        prev = h2;
+    }
+    e = dalloc(M, &M->d_layers, sizeof(LayerDev) * M->L);
+    if (e == hipSuccess) e = hipMemcpy(M->d_layers, ld.data(), sizeof(LayerDev) * M->L, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = dalloc(M, &M->step_bar, kStepBarBytes);
+    if (e == hipSuccess) e = hipMemset(M->step_bar, 0, kStepBarBytes);
+    if (e != hipSuccess) return e;
+    int clock_khz = 0;
+    if ((e = hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, M->device)) != hipSuccess) return e;
+    StepArgs& a = M->step_args;
+    a = StepArgs{};
+    a.layers = M->d_layers;
+    a.n_layers = M->L;
+    a.embed.w = M->embd;
+    a.embed.hidden = M->H;
+    a.embed.h = M->arena_h0;
+    a.embed.ctl = M->d_ctl;
+    a.embed.inv_freq = M->inv_freq;
+    a.embed.rope = M->rope;
+    a.embed.half_rot = M->rot / 2;
+    a.head_mv = M->mv_head;
+    a.head_mv.x = prev;
+    a.head_mv.seg[0].res = nullptr;
+    layout_grid(a.head_mv, n_wg);
+    a.bar = M->step_bar;
+    a.timeout_ticks = (uint64_t)(clock_khz > 0 ? clock_khz : 100000) * 1000ull * 2ull;   // 2 s
+    a.ctl = M->d_ctl;
+    M->step_key = key;
+    M->step_lds = lds;
+    M->step_wg = n_wg;
+    return hipSuccess;
+}
+
 // One step of the token loop for the active sequence (decode.rs:550-640):
 // embedding (+rope table) -> L x [QKV(+norm) -> attention(+q/k norm, rope, KV
 // append) -> O(+residual) -> gate/up(+norm,+SwiGLU) -> down(+residual)]
@@ -434,6 +575,37 @@ hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
         it = M->graphs.emplace(key, ex).first;
     }
     return hipGraphLaunch(it->second, M->stream);
+}
+
+// One token step of the active sequence: the persistent step kernel when the
+// model has one, else the launch chain (graph replay; eager when tracing).
+// trace (device, (L+1) x hidden): residual stream after the embedding and
+// after every layer.
+hipError_t run_step(ribn_rocm_model* M, bool head, int ctx, float* trace) {
+    if (M->step_wg > 0) {
+        StepArgs a = M->step_args;
+        a.head = head ? 1 : 0;
+        hipError_t e = launch_step(a, M->step_key, M->step_wg, M->step_lds, M->stream);
+        if (e != hipSuccess || !trace) return e;
+        e = hipMemcpyAsync(trace, M->arena_h0, sizeof(float) * M->H, hipMemcpyDeviceToDevice, M->stream);
+        for (int l = 0; e == hipSuccess && l < M->L; l++)
+            e = hipMemcpyAsync(trace + (size_t)(l + 1) * M->H, M->arena_h2[l], sizeof(float) * M->H,
+                               hipMemcpyDeviceToDevice, M->stream);
+        return e;
+    }
+    if (trace) return enqueue_step(M, head, splits_for_ctx(ctx), trace);
+    return graph_step(M, head, ctx);
+}
+
+// A persistent step whose grid barrier gave up (see step.h) sets a flag on the
+// device; checked after the stream is synchronized.
+hipError_t step_failed(ribn_rocm_model* M, bool* failed) {
+    *failed = false;
+    if (M->step_wg == 0) return hipSuccess;
+    uint32_t flag = 0;
+    hipError_t e = hipMemcpy(&flag, M->step_bar + 64, 4, hipMemcpyDeviceToHost);
+    *failed = flag != 0;
+    return e;
 }
 
 // Point the graphs at `slot` and (re)write its device state from the pinned mirror.
@@ -663,7 +835,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     }
     HIPCHK(dalloc(M, &M->counters, sizeof(uint32_t) * n_counters));
     HIPCHK(hipMemsetAsync(M->counters, 0, sizeof(uint32_t) * n_counters, M->stream));
-    HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * ((size_t)M->V / 2 + 64)));
+    HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * std::max<size_t>((size_t)M->V / 2 + 64, 8192)));
 
     const int slots = (int)M->max_seqs + 1;
     HIPCHK(dalloc(M, &M->d_slots, sizeof(SeqState) * slots));
@@ -695,6 +867,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     for (int s = (int)M->max_seqs - 1; s >= 0; s--) M->free_slots.push_back(s);
     for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
     build_launches(M);
+    HIPCHK(build_step(M, (o.flags & RIBN_LOAD_LAUNCH_CHAIN) == 0));
     *out = Mp.release();
     return RIBN_OK;
 }
@@ -723,6 +896,8 @@ extern "C" int ribn_rocm_info(const ribn_rocm_model* M, ribn_rocm_info_t* o) {
     o->weight_bytes = M->weight_bytes;
     o->kv_bytes = M->kv_bytes;
     o->kv_f16 = M->kv_f16 ? 1 : 0;
+    o->persistent_step = M->step_wg > 0 ? 1 : 0;
+    o->step_workgroups = (uint32_t)M->step_wg;
     return RIBN_OK;
 }
 
@@ -753,10 +928,10 @@ extern "C" int ribn_rocm_generate(ribn_rocm_model* M, const uint32_t* prompt, ui
     if (e == hipSuccess) e = reset_slot(M, slot, pages, prompt, n_prompt);
     if (e == hipSuccess) e = select_slot(M, slot);
     if (e == hipSuccess) e = hipEventRecord(e0, M->stream);
-    for (uint32_t p = 0; e == hipSuccess && p + 1 < n_prompt; p++) e = graph_step(M, false, (int)p + 1);
-    if (e == hipSuccess) e = graph_step(M, true, (int)n_prompt);
+    for (uint32_t p = 0; e == hipSuccess && p + 1 < n_prompt; p++) e = run_step(M, false, (int)p + 1, nullptr);
+    if (e == hipSuccess) e = run_step(M, true, (int)n_prompt, nullptr);
     if (e == hipSuccess) e = hipEventRecord(e1, M->stream);
-    for (uint32_t t = 1; e == hipSuccess && t < n_new; t++) e = graph_step(M, true, (int)(n_prompt + t));
+    for (uint32_t t = 1; e == hipSuccess && t < n_new; t++) e = run_step(M, true, (int)(n_prompt + t), nullptr);
     if (e == hipSuccess) e = hipEventRecord(e2, M->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(out_tokens, M->d_tokens + (size_t)slot * (M->context + 1) + n_prompt, sizeof(uint32_t) * n_new,
@@ -771,8 +946,11 @@ extern "C" int ribn_rocm_generate(ribn_rocm_model* M, const uint32_t* prompt, ui
         timing->prefill_tokens = n_prompt;
         timing->decode_tokens = n_new - 1;
     }
+    bool barrier_failed = false;
+    if (e == hipSuccess) e = step_failed(M, &barrier_failed);
     cleanup();
     if (e != hipSuccess) return fail(M, err, err_len, hip_msg("generate", e));
+    if (barrier_failed) return fail(M, err, err_len, "decode step: a grid barrier wait exceeded its limit");
     return RIBN_OK;
 }
 
@@ -794,7 +972,7 @@ extern "C" int ribn_rocm_trace(ribn_rocm_model* M, const uint32_t* tokens, uint3
     if (e == hipSuccess) e = select_slot(M, slot);
     uint32_t* dtok = M->d_tokens + (size_t)slot * (M->context + 1);
     for (uint32_t p = 0; e == hipSuccess && p < n; p++) {
-        e = enqueue_step(M, true, splits_for_ctx((int)p + 1), dtrace);
+        e = run_step(M, true, (int)p + 1, dtrace);
         if (e == hipSuccess)
             e = hipMemcpyAsync(&M->h_out[0], &M->d_slots[slot].last_token, 4, hipMemcpyDeviceToHost, M->stream);
         if (e == hipSuccess && logits_out)
@@ -811,7 +989,10 @@ extern "C" int ribn_rocm_trace(ribn_rocm_model* M, const uint32_t* tokens, uint3
     }
     if (dtrace) hipFree(dtrace);
     give_pages(M, pages);
+    bool barrier_failed = false;
+    if (e == hipSuccess) e = step_failed(M, &barrier_failed);
     if (e != hipSuccess) return fail(M, err, err_len, hip_msg("trace", e));
+    if (barrier_failed) return fail(M, err, err_len, "decode step: a grid barrier wait exceeded its limit");
     return RIBN_OK;
 }
 
@@ -945,7 +1126,7 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
         const uint32_t end = it.prefix + it.token_budget;
         for (uint32_t p = it.prefix; e == hipSuccess && p < end; p++) {
             const bool head = (p + 1 == end) && it.output_budget > 0;
-            e = graph_step(M, head, (int)p + 1);
+            e = run_step(M, head, (int)p + 1, nullptr);
         }
         if (e == hipSuccess && it.output_budget > 0)
             e = hipMemcpyAsync(&M->h_out[r], &M->d_slots[s.slot].last_token, 4, hipMemcpyDeviceToHost, M->stream);
@@ -970,7 +1151,10 @@ extern "C" int ribn_rocm_poll(ribn_rocm_model* M, uint64_t submission, ribn_rocm
     const std::vector<ribn_rocm_batch_item> items = M->pending.items;
     M->has_pending = false;
     for (auto& it : items) M->seqs[it.sequence].in_flight = false;
+    bool barrier_failed = false;
+    if (e == hipSuccess) e = step_failed(M, &barrier_failed);
     if (e != hipSuccess) return fail(M, err, err_len, hip_msg("poll", e));
+    if (barrier_failed) return fail(M, err, err_len, "decode step: a grid barrier wait exceeded its limit");
     for (size_t r = 0; r < items.size(); r++) {
         const auto& it = items[r];
         Sequence& s = M->seqs[it.sequence];
@@ -1255,5 +1439,38 @@ extern "C" int ribn_rocm_argmax(const float* logits, uint64_t n, uint32_t* out, 
     HIPCHK(hipMemcpy(dl, logits, sizeof(float) * n, hipMemcpyHostToDevice));
     HIPCHK(launch_argmax(dl, (uint32_t)n, part, ctr, dout, nullptr));
     HIPCHK(hipMemcpy(out, dout, 4, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
+
+// Per-stage timing of one persistent decode step on the scratch sequence (which
+// must hold `ctx` positions, e.g. after ribn_rocm_generate): workgroup 0's wall
+// clock at the start and after each stage (5 per layer, then the head), in
+// nanoseconds from the start. *n receives 2 + 5 L.
+extern "C" int ribn_rocm_step_stamps(ribn_rocm_model* M, uint32_t ctx, double* out_ns, size_t cap, size_t* n,
+                                     char* err, size_t err_len) {
+    if (!M || !out_ns || !n) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->step_wg == 0) return fail(nullptr, err, err_len, "this model runs the launch chain", RIBN_ERR_INVALID);
+    const size_t count = 2 + 5 * (size_t)M->L;
+    if (cap < count) return fail(nullptr, err, err_len, "stamp array too small", RIBN_ERR_INVALID);
+    if (ctx < 1 || ctx > M->context) return fail(nullptr, err, err_len, "ctx outside the context", RIBN_ERR_INVALID);
+    const int slot = (int)M->max_seqs;
+    uint64_t* d = nullptr;
+    HIPCHK(hipMalloc(&d, sizeof(uint64_t) * count));
+    SeqState s = M->h_state[slot];
+    s.pos = (int)ctx - 1;
+    HIPCHK(hipMemcpy(&M->d_slots[slot], &s, sizeof(SeqState), hipMemcpyHostToDevice));
+    HIPCHK(select_slot(M, slot));
+    StepArgs a = M->step_args;
+    a.head = 1;
+    a.stamps = d;
+    HIPCHK(launch_step(a, M->step_key, M->step_wg, M->step_lds, M->stream));
+    HIPCHK(hipStreamSynchronize(M->stream));
+    std::vector<uint64_t> h(count);
+    HIPCHK(hipMemcpy(h.data(), d, sizeof(uint64_t) * count, hipMemcpyDeviceToHost));
+    hipFree(d);
+    int khz = 0;
+    HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, M->device));
+    for (size_t i = 0; i < count; i++) out_ns[i] = (double)(h[i] - h[0]) * 1e6 / (double)khz;
+    *n = count;
     return RIBN_OK;
 }

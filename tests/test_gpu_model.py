@@ -75,21 +75,36 @@ def _oracle_trace(path, tokens, ctx, hidden=False, kv_round=0):
     return np.stack(ls), (np.stack(hs) if hidden else None)
 
 
+STEPS = ["persistent", "chain"]
+# (model, kv) configurations without a compiled persistent step kernel: they run the launch chain
+NO_STEP_KERNEL = {("qwen3_g8_tied", "bf16")}
+
+
+def _check_path(m, name, kv, step):
+    """The requested step path is the one that runs (persistent kernel when one is compiled)."""
+    want = int(step == "persistent" and (name, kv) not in NO_STEP_KERNEL)
+    assert m.info.persistent_step == want, (name, kv, step, m.info.persistent_step)
+    if want:
+        assert m.info.step_workgroups >= 256
+
+
 def _rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
+@pytest.mark.parametrize("step", STEPS)
 @pytest.mark.parametrize("kv", list(KV_MODES))
 @pytest.mark.parametrize("name", list(MODELS))
-def test_trace_hidden_and_logits(model_paths, name, kv):
+def test_trace_hidden_and_logits(model_paths, name, kv, step):
     path = model_paths[name]
     kv_round, tol = KV_MODES[kv]
     rng = np.random.default_rng(1)
     info_v = MODELS[name]["vocab"]
     tokens = rng.integers(0, info_v, 40).tolist()
-    say(f"trace {name} kv={kv}")
-    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=2, kv=kv) as m:
+    say(f"trace {name} kv={kv} step={step}")
+    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=2, kv=kv, step=step) as m:
         assert m.info.kv_f16 == int(kv == "f16")
+        _check_path(m, name, kv, step)
         am, lg, hd = m.trace(tokens, logits=True, hidden=True)
     ref_l, ref_h = _oracle_trace(path, tokens, 128, hidden=True, kv_round=kv_round)
     for layer in range(ref_h.shape[1]):
@@ -107,15 +122,17 @@ def test_trace_hidden_and_logits(model_paths, name, kv):
         assert am[p] == orc.argmax(lg[p])   # the device argmax is the argmax of the device logits
 
 
+@pytest.mark.parametrize("step", STEPS)
 @pytest.mark.parametrize("kv", list(KV_MODES))
-def test_long_context_split_k(model_paths, kv):
-    """700 positions: 32 splits over 44 pages, log-sum-exp merge across workgroups."""
+def test_long_context_split_k(model_paths, kv, step):
+    """700 positions: 16 splits over 44 pages, log-sum-exp merge across workgroups."""
     path = model_paths["qwen3_q4km_hd128_g4"]
     kv_round, tol = KV_MODES[kv]
     rng = np.random.default_rng(2)
     tokens = rng.integers(0, 1024, 700).tolist()
-    say(f"trace 700 tokens kv={kv}")
-    with ribn_amd.QwenRocm(path, context_tokens=1024, max_sequences=1, kv=kv) as m:
+    say(f"trace 700 tokens kv={kv} step={step}")
+    with ribn_amd.QwenRocm(path, context_tokens=1024, max_sequences=1, kv=kv, step=step) as m:
+        _check_path(m, "qwen3_q4km_hd128_g4", kv, step)
         _, lg, _ = m.trace(tokens, logits=True)
     ref_l, _ = _oracle_trace(path, tokens, 1024, kv_round=kv_round)
     for lo in (0, 100, 300, 600):
@@ -138,19 +155,21 @@ def _oracle_greedy(path, prompt, n_new, ctx, kv_round=0):
     return out, logits
 
 
+@pytest.mark.parametrize("step", STEPS)
 @pytest.mark.parametrize("kv", list(KV_MODES))
 @pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen2_q8_0_g7", "qwen2_0p5b_shape_q8_0"])
-def test_greedy_64_tokens(model_paths, name, kv):
+def test_greedy_64_tokens(model_paths, name, kv, step):
     path = model_paths[name]
     kv_round, tol = KV_MODES[kv]
     rng = np.random.default_rng(3)
     prompt = rng.integers(0, MODELS[name]["vocab"], 16).tolist()
-    say(f"greedy {name} kv={kv}")
-    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=1, kv=kv) as m:
+    say(f"greedy {name} kv={kv} step={step}")
+    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=1, kv=kv, step=step) as m:
+        _check_path(m, name, kv, step)
         toks, timing = m.generate(prompt, 64)
         toks2, _ = m.generate(prompt, 64)
         _, lg, _ = m.trace(prompt + toks.tolist()[:-1], logits=True)
-    assert np.array_equal(toks, toks2), "graph replays are not deterministic"
+    assert np.array_equal(toks, toks2), "repeated runs are not deterministic"
     ref, ref_logits = _oracle_greedy(path, prompt, 64, 128, kv_round)
     err = np.abs(lg[len(prompt) - 1:] - np.stack(ref_logits)[: lg.shape[0] - len(prompt) + 1]).max()
     for i, (a, b) in enumerate(zip(toks.tolist(), ref)):
