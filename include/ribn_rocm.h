@@ -196,13 +196,13 @@ int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, 
 int ribn_rocm_bench_model_kernel(ribn_rocm_model *model, uint32_t which, uint32_t iters, double *avg_ms,
                                  uint64_t *bytes, char *err, size_t err_len);
 
-/* Per-stage timing of one persistent decode step (no reference counterpart:
- * a profiling aid). Runs one step of the scratch sequence at context `ctx`
- * (the sequence must hold ctx positions, e.g. after ribn_rocm_generate) and
- * writes workgroup 0's wall clock in ns from the step's start: at the start,
- * after each of the 5 stages of every layer (QKV, attention, O, gate/up,
- * down) and after the head; *n = 2 + 5 * layers. RIBN_ERR_INVALID if the model
- * runs the launch chain. */
+/* Timing of one persistent decode step (no reference counterpart: a
+ * profiling aid). Runs one step of the scratch sequence at context `ctx` (the
+ * sequence must hold ctx positions, e.g. after ribn_rocm_generate) and writes
+ * workgroup 0's wall clock in ns from the step's start at each mark: the start,
+ * every grid-barrier arrival and release, every end of input staging and every
+ * stage end. cap must be at least 64 * (layers + 1); *n receives the number of
+ * marks. RIBN_ERR_INVALID if the model runs the launch chain. */
 int ribn_rocm_step_stamps(ribn_rocm_model *model, uint32_t ctx, double *out_ns, size_t cap, size_t *n,
                           char *err, size_t err_len);
 

@@ -360,8 +360,8 @@ class QwenRocm:
         return am, lg, hd
 
     def step_stamps(self, ctx: int):
-        """Per-stage wall-clock stamps (ns) of one persistent step at context ctx (see ribn_rocm_step_stamps)."""
-        cap = 2 + 5 * self.info.layers
+        """Wall-clock marks (ns) of one persistent step at context ctx (see ribn_rocm_step_stamps)."""
+        cap = 64 * (self.info.layers + 1)
         out = (ctypes.c_double * cap)()
         n = ctypes.c_size_t()
         self._call(_lib.ribn_rocm_step_stamps, ctx, out, cap, ctypes.byref(n))

@@ -138,13 +138,14 @@ __device__ float deq_elem(const QMat& w, uint32_t row, uint32_t e) {
 
 // ---------------------------------------------------------------------------
 // Matvec input staging. x (optionally the RMSNorm input: rms_norm model_ops.rs:108,
-// x * (1/sqrt(sum/n + eps)) * w) is cut into groups of 16 values; each group gets
-// an fp32 scale s = max|v|/127 and two int8 parts, v ~ s (hi + lo/256), i.e.
-// about 15 significant bits, and the fp32 sum X of its values (for the Q4_K
-// minima and the Q6_K offset). The products with the quants then run on
-// v_dot4_i32_i8 with exact int32 accumulation. For an RMSNorm input the group
-// holds x*w and the normalisation factor 1/sqrt(mean(x^2)+eps) is returned as
-// an output multiplier, so x is read once.
+// x * (1/sqrt(sum/n + eps)) * w) is stored in 16-bit fixed point: each block of
+// 64 values has an fp32 scale s = max|v| / 32512 and v ~ s v16 with v16 =
+// rint(v / s) (resolution 3e-5 of the block maximum), kept as two signed bytes
+// v16 = 256 hi + lo. Every group of 16 values also keeps the fp32 sum X of its
+// values (for the Q4_K minima and the Q6_K offset). Products with the quants run
+// on v_dot4_i32_i8 and are exact in int32. For an RMSNorm input the blocks hold
+// x*w and the normalisation factor 1/sqrt(mean(x^2)+eps) is returned as an
+// output multiplier, so x is read once.
 //
 // LDS layout: [k] int8 parts in unit planes | [k/16] (s, X) pairs | 64 fp32
 // reduction slots. Unit planes: plane j (Q4_K/Q6_K: 0..3, Q8_0: 0..1) holds,
@@ -175,21 +176,26 @@ __device__ __forceinline__ void plane_of_group(int g, int& unit, int& plane, int
 }
 
 template <int T>
-__device__ float stage_x(const MvArgs& a, int8_t* xs, float* gs, float* red) {
-    const int k = a.k, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
-    const bool norm = a.norm_w != nullptr;
+__device__ float stage_x(const float* x, const float* norm_w, float eps, int k, int8_t* xs, float* gs, float* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(norm_w);
+    const bool norm = norm_w != nullptr;
     const int n_units = T == 8 ? k / 16 : k / 32;
+    const int n16 = k / 16;
     u4_t* planes = reinterpret_cast<u4_t*>(xs);
     float ss = 0.f;
-    for (int g = tid; g < k / 16; g += kThreads) {
+    // thread = one group of 16 values; the four groups of a 64-value block sit in
+    // four consecutive lanes, which share the block's scale
+    for (int base = 0; base < n16; base += kThreads) {
+        const int g = base + tid;
+        const bool valid = g < n16;
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float4 t = x4[g * 4 + j];
+            float4 t = valid ? x4[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
             ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-            if (norm) {
+            if (norm && valid) {
                 const float4 w = w4[g * 4 + j];
                 t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
             }
@@ -201,33 +207,39 @@ __device__ float stage_x(const MvArgs& a, int8_t* xs, float* gs, float* red) {
             am = fmaxf(am, fabsf(v[j]));
             sum += v[j];
         }
-        const float sc = am * (1.0f / 127.0f);
-        const float is = am > 0.f ? 127.0f / am : 0.f;
+        // maximum over the 4 lanes of a quad: DPP quad permutes (lane ^ 1, lane ^ 2)
+        am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0xB1, 0xF, 0xF, true)));
+        am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x4E, 0xF, 0xF, true)));
+        // x ~ s * v16 with v16 = rint(x / s) in [-32512, 32512], s = max|x| / 32512
+        // over the 64-value block; v16 = 256 hi + lo with hi, lo signed bytes
+        const float sc = am * (1.0f / 32512.0f);
+        const float is = am > 0.f ? 32512.0f / am : 0.f;
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t h4 = 0, l4 = 0;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                const float vv = v[4 * j + b];
-                const float hq = rintf(vv * is);
-                const float lq = fminf(fmaxf(rintf((vv - hq * sc) * is * 256.0f), -127.f), 127.f);
-                h4 |= ((uint32_t)(int32_t)hq & 0xffu) << (8 * b);
-                l4 |= ((uint32_t)(int32_t)lq & 0xffu) << (8 * b);
+                const int q = (int)rintf(v[4 * j + b] * is);
+                const int hi = (q + 128) >> 8, lo = q - (hi << 8);
+                h4 |= ((uint32_t)hi & 0xffu) << (8 * b);
+                l4 |= ((uint32_t)lo & 0xffu) << (8 * b);
             }
             hw[j] = h4;
             lw[j] = l4;
         }
-        int unit, plane, slot;
-        plane_of_group<T>(g, unit, plane, slot);
-        planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
-        planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
-        if constexpr (T == 8) {
-            gs[unit * 2] = sc;
-            gs[unit * 2 + 1] = sum;
-        } else {
-            gs[unit * 4 + slot] = sc;
-            gs[unit * 4 + 2 + slot] = sum;
+        if (valid) {
+            int unit, plane, slot;
+            plane_of_group<T>(g, unit, plane, slot);
+            planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
+            planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
+            if constexpr (T == 8) {
+                gs[unit * 2] = sc;
+                gs[unit * 2 + 1] = sum;
+            } else {
+                gs[unit * 4 + slot] = sc;
+                gs[unit * 4 + 2 + slot] = sum;
+            }
         }
     }
     float inv = 1.0f;
@@ -238,25 +250,27 @@ __device__ float stage_x(const MvArgs& a, int8_t* xs, float* gs, float* red) {
         ss = 0.f;
 #pragma unroll
         for (int i = 0; i < kWaves; i++) ss += red[i];
-        inv = 1.0f / sqrtf(ss / (float)k + a.eps);
+        inv = 1.0f / sqrtf(ss / (float)k + eps);
     }
     __syncthreads();
     return inv;
 }
 
-// sum_j q_j x_j over 16 values for int8 bytes q (4 per dword) and x parts.
-__device__ __forceinline__ int dot16i(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& x) {
-    int acc = __builtin_amdgcn_sdot4((int)q0, (int)x.x, 0, false);
-    acc = __builtin_amdgcn_sdot4((int)q1, (int)x.y, acc, false);
-    acc = __builtin_amdgcn_sdot4((int)q2, (int)x.z, acc, false);
-    acc = __builtin_amdgcn_sdot4((int)q3, (int)x.w, acc, false);
-    return acc;
-}
-// s * sum_j q_j v_j for a group staged as v ~ s (hi + lo/256)
-__device__ __forceinline__ float dot16s(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& xh,
-                                        const u4_t& xl) {
-    const int h = dot16i(q0, q1, q2, q3, xh), l = dot16i(q0, q1, q2, q3, xl);
-    return fmaf((float)l, 1.0f / 256.0f, (float)h);
+// sum_j q_j v16_j over 16 values, exact in int32: q are bytes (4 per dword),
+// v16 = 256 hi + lo with the hi and lo bytes in xh and xl. The lo products
+// accumulate onto the hi sum shifted by 8.
+__device__ __forceinline__ int dot16v(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, const u4_t& xh,
+                                      const u4_t& xl) {
+    int h = __builtin_amdgcn_sdot4((int)q0, (int)xh.x, 0, false);
+    h = __builtin_amdgcn_sdot4((int)q1, (int)xh.y, h, false);
+    h = __builtin_amdgcn_sdot4((int)q2, (int)xh.z, h, false);
+    h = __builtin_amdgcn_sdot4((int)q3, (int)xh.w, h, false);
+    int t = h << 8;
+    t = __builtin_amdgcn_sdot4((int)q0, (int)xl.x, t, false);
+    t = __builtin_amdgcn_sdot4((int)q1, (int)xl.y, t, false);
+    t = __builtin_amdgcn_sdot4((int)q2, (int)xl.z, t, false);
+    t = __builtin_amdgcn_sdot4((int)q3, (int)xl.w, t, false);
+    return t;
 }
 
 // ---------------------------------------------------------------------------
@@ -302,17 +316,18 @@ struct Unit<12> {
     }
     static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
         const float d = h2f(r.dd), dmin = h2f(r.dd >> 16);
-        const float4 G = reinterpret_cast<const float4*>(gs)[u];   // s_a, s_b, X_a, X_b
+        const float4 G = reinterpret_cast<const float4*>(gs)[u];   // s, s, X_a, X_b
         const uint32_t m = 0x0f0f0f0fu;
-        const float t0 = dot16s(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m, xs4[u], xs4[U + u]);
-        const float t1 = dot16s((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m, xs4[2 * U + u],
-                                xs4[3 * U + u]);
-        // sum_j x_j ((d sc) q_j - dmin m) = (d sc) s t - (dmin m) X, per group
-        acc = fmaf(d * (float)(r.s & 0xffu) * G.x, t0, acc);
-        acc = fmaf(-dmin * (float)((r.s >> 16) & 0xffu), G.z, acc);
-        acc = fmaf(d * (float)((r.s >> 8) & 0xffu) * G.y, t1, acc);
-        acc = fmaf(-dmin * (float)(r.s >> 24), G.w, acc);
-        return acc;
+        // q in [0, 15], |v16| <= 32639: |t| < 2^23, so 24-bit products are exact
+        const int ta = dot16v(r.q.x & m, r.q.y & m, r.q.z & m, r.q.w & m, xs4[u], xs4[U + u]);
+        const int tb = dot16v((r.q.x >> 4) & m, (r.q.y >> 4) & m, (r.q.z >> 4) & m, (r.q.w >> 4) & m, xs4[2 * U + u],
+                              xs4[3 * U + u]);
+        // both halves of a unit lie in one 64-value block of x (one scale s):
+        // sum_j x_j ((d sc) q_j - dmin m) = d s (sc_a t_a + sc_b t_b) - dmin (m_a X_a + m_b X_b)
+        const int comb = __mul24((int)(r.s & 0xffu), ta) + __mul24((int)((r.s >> 8) & 0xffu), tb);
+        acc = fmaf(d * G.x, (float)comb, acc);
+        const float mins = fmaf((float)(r.s >> 24), G.w, (float)((r.s >> 16) & 0xffu) * G.z);
+        return fmaf(-dmin, mins, acc);
     }
 };
 
@@ -344,8 +359,8 @@ struct Unit<14> {
         const float d = h2f(r.d);
         const float scl = (float)(int8_t)(r.sc & 0xffu), sch = (float)(int8_t)(r.sc >> 8);
         const float4 G = reinterpret_cast<const float4*>(gs)[u];
-        const float t0 = dot16s(lo[0], lo[1], lo[2], lo[3], xs4[u], xs4[U + u]);
-        const float t1 = dot16s(hi[0], hi[1], hi[2], hi[3], xs4[2 * U + u], xs4[3 * U + u]);
+        const float t0 = (float)dot16v(lo[0], lo[1], lo[2], lo[3], xs4[u], xs4[U + u]);
+        const float t1 = (float)dot16v(hi[0], hi[1], hi[2], hi[3], xs4[2 * U + u], xs4[3 * U + u]);
         // sum_j x_j (d sc)(q_j - 32) = (d sc)(s t - 32 X), per 16-value sub-block
         acc = fmaf(d * scl, fmaf(G.x, t0, -32.0f * G.z), acc);
         acc = fmaf(d * sch, fmaf(G.y, t1, -32.0f * G.w), acc);
@@ -365,7 +380,7 @@ struct Unit<8> {
     }
     static __device__ __forceinline__ float apply(const Raw& r, int u, const u4_t* xs4, int U, const float* gs, float acc) {
         const float2 G = reinterpret_cast<const float2*>(gs)[u];
-        const float t = dot16s(r.q.x, r.q.y, r.q.z, r.q.w, xs4[u], xs4[U + u]);
+        const float t = (float)dot16v(r.q.x, r.q.y, r.q.z, r.q.w, xs4[u], xs4[U + u]);
         return fmaf(h2f(r.d) * G.x, t, acc);
     }
 };
@@ -379,8 +394,8 @@ struct Group {
 // Where a wave's work lives: items (two rows each, or one gate/up pair) of one
 // segment, walked as a flat sequence of load groups. Every field is wave-uniform.
 struct WaveWork {
-    const QMat* wa;
-    const QMat* wb;        // second row's matrix (the up matrix for gate/up pairs)
+    QMat wa;
+    QMat wb;               // second row's matrix (the up matrix for gate/up pairs)
     int first_item, n_items, n_rows, ngr, n_units;
     bool pair;
 };
@@ -398,10 +413,10 @@ __device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int i
     const int lane = threadIdx.x & 63;
     const int g0 = gi * 128, g1 = g0 + 64 < w.n_units ? g0 + 64 : 0;
     const int l0 = g0 + lane < w.n_units ? lane : 0, l1 = g1 + lane < w.n_units ? lane : 0;
-    g.a0 = U::load_full(*w.wa, (size_t)ra, g0, l0);
-    g.b0 = U::load_full(*w.wb, (size_t)rb, g0, l0);
-    g.a1 = U::load_full(*w.wa, (size_t)ra, g1, l1);
-    g.b1 = U::load_full(*w.wb, (size_t)rb, g1, l1);
+    g.a0 = U::load_full(w.wa, (size_t)ra, g0, l0);
+    g.b0 = U::load_full(w.wb, (size_t)rb, g0, l0);
+    g.a1 = U::load_full(w.wa, (size_t)ra, g1, l1);
+    g.b1 = U::load_full(w.wb, (size_t)rb, g1, l1);
 }
 
 // Position (item, group) of a wave's walk, advanced one load group at a time.
@@ -412,78 +427,141 @@ struct Cursor {
     }
 };
 
-// The wave's load groups live in a ring of P register slots: slot j is
-// computed, then refilled with the group P positions ahead, so P-1 groups of
-// 128-bit loads are in flight while one is computed. The first P groups are
-// issued before the workgroup waits for its input (mv_run).
-template <int T, int MODE, int P>
-__device__ __forceinline__ void mv_body(const MvSeg& sg, const WaveWork& w, Group<T> (&ring)[P], Cursor ld,
-                                        const u4_t* xs4, const float* gs, float oscale, uint64_t& best) {
-    using U = Unit<T>;
+// The wave's load groups live in a ring of D register slots: slot j is
+// computed, then refilled with the group D positions ahead, so D-1 groups of
+// 128-bit loads are in flight while one is computed. Every full round issues
+// the same D refills (the last one's refills past the end reload the wave's
+// last group, which the L2 still holds) and the final round issues none, so
+// the compiler's wait counting sees a fixed number of loads behind each slot
+// and waits for that slot only. With refills that depend on the position it
+// has to assume none was issued and waits for every load in flight.
+// Addend of each output row a wave produces (residual for MV_ADD plus bias),
+// loaded before the wave's first weight loads so that its latency overlaps
+// them: lane 2i holds item i's first row, lane 2i+1 its second (a gate/up
+// item's single row in lane 2i). Needs at most 32 items per wave.
+__device__ __forceinline__ float mv_addend(const MvSeg& sg, const WaveWork& w, int mode) {
     const int lane = threadIdx.x & 63;
-    const int total = w.n_items * w.ngr;
-    float a0 = 0.f, b0 = 0.f;
-    Cursor c{0, 0};
-    for (int q0 = 0; q0 < total; q0 += P) {
+    float v = 0.f;
+    if (lane < 2 * w.n_items) {
+        const int item = w.first_item + (lane >> 1) * kWaves;
+        const int row = w.pair ? item : 2 * item + (lane & 1);
+        if (row < w.n_rows && !(w.pair && (lane & 1))) {
+            if (mode == MV_ADD) v = sg.res[row];
+            if (sg.bias) v += sg.bias[row];
+        }
+    }
+    return v;
+}
+
+template <int T, int MODE>
+__device__ __forceinline__ void mv_finish(const MvSeg& sg, const WaveWork& w, const Cursor& c, float& a0, float& b0,
+                                          float oscale, float addend, uint64_t& best) {
+    if (c.gi != w.ngr - 1) return;
+    const int lane = threadIdx.x & 63;
+    // both row sums in one reduction: after the xor-32 step lanes 0-31 hold
+    // row a, lanes 32-63 row b
+    const bool lo_half = lane < 32;
+    const float send = lo_half ? b0 : a0;
+    float v = (lo_half ? a0 : b0) + __shfl_xor(send, 32);
 #pragma unroll
-        for (int j = 0; j < P; j++) {
-            // one slot at a time: without this fence the scheduler interleaves
-            // the LDS reads of all P slots and the register demand multiplies
-            __builtin_amdgcn_sched_barrier(0);
-            if (q0 + j < total) {
-                const int u0 = c.gi * 128 + lane, u1 = u0 + 64;
-                if (u0 < w.n_units) {
-                    a0 = U::apply(ring[j].a0, u0, xs4, w.n_units, gs, a0);
-                    b0 = U::apply(ring[j].b0, u0, xs4, w.n_units, gs, b0);
-                }
-                if (u1 < w.n_units) {
-                    a0 = U::apply(ring[j].a1, u1, xs4, w.n_units, gs, a0);
-                    b0 = U::apply(ring[j].b1, u1, xs4, w.n_units, gs, b0);
-                }
-                if (q0 + j + P < total) {
-                    // keep the refill after the slot's last use: otherwise the
-                    // scheduler hoists it and holds two copies of every slot
-                    __builtin_amdgcn_sched_barrier(0);
-                    load_group<T>(ring[j], w, ld.it, ld.gi);
-                    ld.next(w.ngr);
-                }
-                if (c.gi == w.ngr - 1) {
-                    float ya = wave_sum(a0) * oscale, yb = wave_sum(b0) * oscale;
-                    a0 = b0 = 0.f;
-                    const int item = w.first_item + c.it * kWaves;
-                    const int ra = w.pair ? item : 2 * item;
-                    const int rb = w.pair ? item : ra + 1;
-                    if (lane == 0) {
-                        const bool has_b = !w.pair && rb < w.n_rows;
-                        if (sg.bias) {
-                            ya += sg.bias[ra];
-                            if (has_b) yb += sg.bias[rb];
-                        }
-                        // outputs are written through to memory (agent-scope stores)
-                        // so workgroups on other XCDs read them after a grid barrier
-                        if constexpr (MODE == MV_ADD) {
-                            st_agent(sg.out + ra, sg.res[ra] + ya);
-                            if (has_b) st_agent(sg.out + rb, sg.res[rb] + yb);
-                        } else if constexpr (MODE == MV_SILU) {
-                            st_agent(sg.out + ra, ya / (1.0f + expf(-ya)) * yb);
-                        } else {
-                            st_agent(sg.out + ra, ya);
-                            if (has_b) st_agent(sg.out + rb, yb);
-                            if constexpr (MODE == MV_HEAD) {
-                                best = max(best, argmax_key(ya, (uint32_t)ra));
-                                if (has_b) best = max(best, argmax_key(yb, (uint32_t)rb));
-                            }
-                        }
-                    }
-                }
-                c.next(w.ngr);
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const float ya = __shfl(v, 0) * oscale, yb = __shfl(v, 32) * oscale;
+    a0 = b0 = 0.f;
+    const int item = w.first_item + c.it * kWaves;
+    const int ra = w.pair ? item : 2 * item;
+    const int rb = w.pair ? item : ra + 1;
+    // (the host keeps a launch with addends at <= 32 items per wave)
+    const int al = (2 * c.it) & 63;
+    const float add_a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend), al));
+    const float add_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend), al + 1));
+    if (lane == 0) {
+        const bool has_b = !w.pair && rb < w.n_rows;
+        // outputs are written through to memory (agent-scope stores) so
+        // workgroups on other XCDs read them after a grid barrier
+        if constexpr (MODE == MV_ADD) {
+            st_agent(sg.out + ra, add_a + ya);
+            if (has_b) st_agent(sg.out + rb, add_b + yb);
+        } else if constexpr (MODE == MV_SILU) {
+            st_agent(sg.out + ra, ya / (1.0f + expf(-ya)) * yb);
+        } else {
+            const float oa = ya + add_a, ob = yb + add_b;
+            st_agent(sg.out + ra, oa);
+            if (has_b) st_agent(sg.out + rb, ob);
+            if constexpr (MODE == MV_HEAD) {
+                best = max(best, argmax_key(oa, (uint32_t)ra));
+                if (has_b) best = max(best, argmax_key(ob, (uint32_t)rb));
             }
         }
     }
 }
 
-// Issue the first P load groups, wait for the input (sync: a grid barrier in
-// the persistent step, nothing in a standalone launch), stage it, run the ring.
+template <int T>
+__device__ __forceinline__ void mv_group(const Group<T>& g, const WaveWork& w, const Cursor& c, const u4_t* xs4,
+                                         const float* gs, float& a0, float& b0) {
+    using U = Unit<T>;
+    const int u0 = c.gi * 128 + (threadIdx.x & 63), u1 = u0 + 64;
+    if (u0 < w.n_units) {
+        a0 = U::apply(g.a0, u0, xs4, w.n_units, gs, a0);
+        b0 = U::apply(g.b0, u0, xs4, w.n_units, gs, b0);
+    }
+    if (u1 < w.n_units) {
+        a0 = U::apply(g.a1, u1, xs4, w.n_units, gs, a0);
+        b0 = U::apply(g.b1, u1, xs4, w.n_units, gs, b0);
+    }
+}
+
+// Ring of depth D for a wave with total >= D groups, after stage_x.
+template <int T, int MODE, int D, typename Sync>
+__device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const WaveWork& w, int8_t* xs, float* gs,
+                                        float* red, uint64_t& best, Sync&& sync) {
+    const int total = w.n_items * w.ngr;
+    const float addend = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE) : 0.f;
+    Group<T> ring[D];
+    Cursor ld{0, 0};
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+        load_group<T>(ring[j], w, ld.it, ld.gi);
+        ld.next(w.ngr);
+    }
+    int ldq = D;   // index of the group `ld` points at
+    if (!sync()) return false;
+    const float* const x = a.x;
+    const float* const norm_w = a.norm_w;
+    const float eps = a.eps;
+    const int k = a.k;
+    const float oscale = stage_x<T>(x, norm_w, eps, k, xs, gs, red);
+    sync.mark();
+    const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
+    float a0 = 0.f, b0 = 0.f;
+    Cursor c{0, 0};
+    int q0 = 0;
+    for (; q0 + D < total; q0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            mv_group<T>(ring[j], w, c, xs4, gs, a0, b0);
+            load_group<T>(ring[j], w, ld.it, ld.gi);
+            if (ldq + 1 < total) {
+                ld.next(w.ngr);
+                ++ldq;
+            }
+            mv_finish<T, MODE>(sg, w, c, a0, b0, oscale, addend, best);
+            c.next(w.ngr);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < D; j++) {
+        if (q0 + j < total) {
+            mv_group<T>(ring[j], w, c, xs4, gs, a0, b0);
+            mv_finish<T, MODE>(sg, w, c, a0, b0, oscale, addend, best);
+            c.next(w.ngr);
+        }
+    }
+    return true;
+}
+
+// Stage the input and run the wave's groups with a ring of depth P (or less
+// for a wave with fewer groups). The first loads are issued before `sync`
+// (a grid barrier in the persistent step, nothing in a standalone launch).
 // Returns false if sync reports a failed barrier.
 template <int T, int MODE, int P, typename Sync>
 __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWork& w, int8_t* xs, float* gs,
@@ -491,29 +569,32 @@ __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWor
     w.n_units = (int)sg.w.nb * Unit<T>::kPerBlock;
     w.ngr = (w.n_units + 127) / 128;
     const int total = w.n_items * w.ngr;
-    Group<T> ring[P];
-    Cursor ld{0, 0};
-#pragma unroll
-    for (int j = 0; j < P; j++) {
-        if (j < total) {
-            load_group<T>(ring[j], w, ld.it, ld.gi);
-            ld.next(w.ngr);
-        }
+    // depth: one that divides the wave's group count (no refill past the end),
+    // or the full depth when the count is large enough for a few reloads of the
+    // last group not to matter
+    if (total >= P && (total % P == 0 || total >= 3 * P)) return mv_ring<T, MODE, P>(a, sg, w, xs, gs, red, best, sync);
+    if constexpr (P > 3) {
+        if (total >= 3 && total % 3 == 0) return mv_ring<T, MODE, 3>(a, sg, w, xs, gs, red, best, sync);
     }
+    if constexpr (P > 2) {
+        if (total >= 2) return mv_ring<T, MODE, 2>(a, sg, w, xs, gs, red, best, sync);
+    }
+    if (total >= 1) return mv_ring<T, MODE, 1>(a, sg, w, xs, gs, red, best, sync);
+    // no work: take part in the barrier and the workgroup's staging
     if (!sync()) return false;
-    const float oscale = stage_x<T>(a, xs, gs, red);
-    const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
-    mv_body<T, MODE, P>(sg, w, ring, ld, xs4, gs, oscale, best);
+    stage_x<T>(a.x, a.norm_w, a.eps, a.k, xs, gs, red);
+    sync.mark();
     return true;
 }
 
 struct NoSync {
     __device__ __forceinline__ bool operator()() const { return true; }
+    __device__ __forceinline__ void mark() const {}
 };
 
 // One workgroup's share of a matvec launch laid out in `a` (segments, items per
 // wave). Workgroups beyond the layout only sync. LDS: staged input at `lds`.
-template <int TA, int TB, int MODE, int P, typename Sync>
+template <int TA, int TB, int MODE, int PA, int PB, typename Sync>
 __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uint64_t& best, Sync&& sync) {
     int8_t* xs = reinterpret_cast<int8_t*>(lds);
     float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
@@ -521,20 +602,23 @@ __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uin
     int si = 0;
     if (a.nseg > 1 && wg >= a.seg[1].wg_begin) si = 1;
     if (a.nseg > 2 && wg >= a.seg[2].wg_begin) si = 2;
-    const MvSeg& sg = a.seg[si];
+    // descriptors by value: in the persistent step `a` lives in global memory,
+    // where the output stores could alias it, so reads through `a` in the loop
+    // would be reloaded before every weight load
+    const MvSeg sg = a.seg[si];
     const int lwg = wg - sg.wg_begin;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr bool pair = MODE == MV_SILU;
     WaveWork w;
-    w.wa = &sg.w;
-    w.wb = pair ? &sg.w2 : &sg.w;
+    w.wa = sg.w;
+    w.wb = pair ? sg.w2 : sg.w;
     w.pair = pair;
     w.n_rows = (int)sg.w.rows;
     w.first_item = lwg * sg.ipw * kWaves + wave;
     const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
     w.n_items = max(0, min(sg.ipw, (n_item_total - w.first_item + kWaves - 1) / kWaves));
-    if (si == 2 && TB != TA) return mv_run<TB, MODE, P>(a, sg, w, xs, gs, red, best, sync);
-    return mv_run<TA, MODE, P>(a, sg, w, xs, gs, red, best, sync);
+    if (si == 2 && TB != TA) return mv_run<TB, MODE, PB>(a, sg, w, xs, gs, red, best, sync);
+    return mv_run<TA, MODE, PA>(a, sg, w, xs, gs, red, best, sync);
 }
 
 // Greedy token of the head launch: first maximum over the vocabulary, NaN

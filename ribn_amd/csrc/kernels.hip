@@ -5,10 +5,10 @@
 //  * weights stay in their GGUF block encoding, re-tiled at load into
 //    16-byte-aligned planes (kernels.h, QMat) so each lane issues 128-bit
 //    non-temporal loads and a wave reads 1 KiB of contiguous quants;
-//  * the input vector is staged once per workgroup in LDS as two int8 parts
-//    per value with one fp32 scale per 16 values (about 15 significant bits),
-//    and the quants meet it in v_dot4_i32_i8 with exact int32 accumulation;
-//    per-16 fp32 sums of x carry the Q4_K minimum and the Q6_K offset terms;
+//  * the input vector is staged once per workgroup in LDS in 16-bit fixed point
+//    (one fp32 scale per 64 values, two signed bytes per value), and the quants
+//    meet it in v_dot4_i32_i8 with exact int32 accumulation; per-16 fp32 sums
+//    of x carry the Q4_K minimum and the Q6_K offset terms;
 //  * RMSNorm is a workgroup prologue; residual add, SwiGLU and the vocab argmax
 //    are epilogues; q/k head norm, NeoX rope and the KV append live in the
 //    attention prologue, so one layer is 5 launches.
@@ -65,7 +65,7 @@ template <int TA, int TB, int MODE>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint64_t best = 0ull;
-    mv_wg<TA, TB, MODE, kRingStandalone>(a, blockIdx.x, lds, best, NoSync{});
+    mv_wg<TA, TB, MODE, kRingStandalone, kRingStandalone>(a, blockIdx.x, lds, best, NoSync{});
     if constexpr (MODE == MV_HEAD) head_finish(a, best, blockIdx.x, gridDim.x);
 }
 
@@ -161,6 +161,8 @@ int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * kWaves * (a.
 
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
     if (n_wg <= 0 || a.k <= 0 || a.k % 16) return hipErrorInvalidValue;
+    for (int i = 0; i < a.nseg; i++)   // per-row addends are held one per lane (mv_addend)
+        if ((a.mode == MV_ADD || a.seg[i].bias) && a.seg[i].ipw > 32) return hipErrorInvalidValue;
     switch (a.mode) {
     case MV_STORE: return matvec_dispatch<MV_STORE>(a, n_wg, st);
     case MV_ADD: return matvec_dispatch<MV_ADD>(a, n_wg, st);

@@ -332,6 +332,8 @@ int layout_grid(MvArgs& a, int n_wg) {
         wg += wgs[i];
     }
     a.items_per_wave = ipw[0];
+    for (int i = 0; i < a.nseg; i++)   // per-row addends are held one per lane
+        if ((a.mode == MV_ADD || a.seg[i].bias) && a.seg[i].ipw > 32) return -1;
     return wg;
 }
 
@@ -350,7 +352,7 @@ void build_launches(ribn_rocm_model* M) {
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
-        q.items_per_wave = ipw_env("QKV", 1);
+        q.items_per_wave = ipw_env("QKV", 2);
         q.nseg = 3;
         q.type_a = y.q.type;
         q.type_b = y.v.type;
@@ -380,7 +382,7 @@ void build_launches(ribn_rocm_model* M) {
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
         d.type_a = d.type_b = y.down.type;
-        d.items_per_wave = ipw_env("DOWN", 1);
+        d.items_per_wave = ipw_env("DOWN", 2);
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
@@ -456,7 +458,7 @@ hipError_t build_step(ribn_rocm_model* M, bool allow) {
         L.qkv.x = prev;
         L.qkv.seg[0].out = raw; L.qkv.seg[1].out = raw + qd; L.qkv.seg[2].out = raw + qd + kd;
         for (auto& sg : L.qkv.seg) sg.res = nullptr;
-        layout_grid(L.qkv, n_wg);
+        if (layout_grid(L.qkv, n_wg) < 0) return hipSuccess;   // no persistent step for this shape
         L.attn = attn_args(M, l, 1);
         L.attn.raw = raw;
         L.attn.out = att;
@@ -464,17 +466,17 @@ hipError_t build_step(ribn_rocm_model* M, bool allow) {
         L.o.x = att;
         L.o.seg[0].out = h1;
         L.o.seg[0].res = prev;
-        layout_grid(L.o, n_wg);
+        if (layout_grid(L.o, n_wg) < 0) return hipSuccess;   // no persistent step for this shape
         L.gu = M->mv_gu[l];
         L.gu.x = h1;
         L.gu.seg[0].out = act;
         L.gu.seg[0].res = nullptr;
-        layout_grid(L.gu, n_wg);
+        if (layout_grid(L.gu, n_wg) < 0) return hipSuccess;   // no persistent step for this shape
         L.down = M->mv_down[l];
         L.down.x = act;
         L.down.seg[0].out = h2;
         L.down.seg[0].res = h1;
-        layout_grid(L.down, n_wg);
+        if (layout_grid(L.down, n_wg) < 0) return hipSuccess;   // no persistent step for this shape
         M->arena_h2[l] = h2;
         prev = h2;
     }
@@ -499,7 +501,7 @@ hipError_t build_step(ribn_rocm_model* M, bool allow) {
     a.head_mv = M->mv_head;
     a.head_mv.x = prev;
     a.head_mv.seg[0].res = nullptr;
-    layout_grid(a.head_mv, n_wg);
+    if (layout_grid(a.head_mv, n_wg) < 0) return hipSuccess;
     a.bar = M->step_bar;
     a.timeout_ticks = (uint64_t)(clock_khz > 0 ? clock_khz : 100000) * 1000ull * 2ull;   // 2 s
     a.ctl = M->d_ctl;
@@ -1442,20 +1444,22 @@ extern "C" int ribn_rocm_argmax(const float* logits, uint64_t n, uint32_t* out, 
     return RIBN_OK;
 }
 
-// Per-stage timing of one persistent decode step on the scratch sequence (which
-// must hold `ctx` positions, e.g. after ribn_rocm_generate): workgroup 0's wall
-// clock at the start and after each stage (5 per layer, then the head), in
-// nanoseconds from the start. *n receives 2 + 5 L.
+// Timing of one persistent decode step on the scratch sequence (which must
+// hold `ctx` positions, e.g. after ribn_rocm_generate): workgroup 0's wall
+// clock at the step's start, at every barrier arrival and release, after every
+// input staging and at every stage end, in ns from the start. *n receives the
+// number of marks.
 extern "C" int ribn_rocm_step_stamps(ribn_rocm_model* M, uint32_t ctx, double* out_ns, size_t cap, size_t* n,
                                      char* err, size_t err_len) {
     if (!M || !out_ns || !n) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
     if (M->step_wg == 0) return fail(nullptr, err, err_len, "this model runs the launch chain", RIBN_ERR_INVALID);
-    const size_t count = 2 + 5 * (size_t)M->L;
+    const size_t count = 64 * ((size_t)M->L + 1);
     if (cap < count) return fail(nullptr, err, err_len, "stamp array too small", RIBN_ERR_INVALID);
     if (ctx < 1 || ctx > M->context) return fail(nullptr, err, err_len, "ctx outside the context", RIBN_ERR_INVALID);
     const int slot = (int)M->max_seqs;
     uint64_t* d = nullptr;
     HIPCHK(hipMalloc(&d, sizeof(uint64_t) * count));
+    HIPCHK(hipMemset(d, 0, sizeof(uint64_t) * count));
     SeqState s = M->h_state[slot];
     s.pos = (int)ctx - 1;
     HIPCHK(hipMemcpy(&M->d_slots[slot], &s, sizeof(SeqState), hipMemcpyHostToDevice));
@@ -1470,7 +1474,9 @@ extern "C" int ribn_rocm_step_stamps(ribn_rocm_model* M, uint32_t ctx, double* o
     hipFree(d);
     int khz = 0;
     HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, M->device));
-    for (size_t i = 0; i < count; i++) out_ns[i] = (double)(h[i] - h[0]) * 1e6 / (double)khz;
-    *n = count;
+    size_t m = 0;
+    while (m < count && h[m] != 0) m++;
+    for (size_t i = 0; i < m; i++) out_ns[i] = (double)(h[i] - h[0]) * 1e6 / (double)khz;
+    *n = m;
     return RIBN_OK;
 }

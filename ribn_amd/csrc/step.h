@@ -73,7 +73,17 @@ struct GridSync {
     uint32_t* bar;
     uint32_t n;
     uint64_t deadline;
-    __device__ __forceinline__ bool operator()() const { return grid_sync(bar, n, deadline); }
+    uint64_t* stamp;      // profiling (workgroup 0, thread 0 only): wall clock at marks
+    int* ns;
+    __device__ __forceinline__ void mark() const {
+        if (stamp && threadIdx.x == 0) stamp[(*ns)++] = wall_clock64();
+    }
+    __device__ __forceinline__ bool operator()() const {
+        mark();
+        const bool ok = grid_sync(bar, n, deadline);
+        mark();
+        return ok;
+    }
 };
 // The barrier of the first work item only (later items of the same workgroup
 // run after it).
@@ -100,7 +110,17 @@ __device__ __forceinline__ bool attn_items(const AttnArgs& a, int wg, int n_wg, 
     return true;
 }
 
-constexpr int kRingStep = 3;
+// Ring depth (load groups per wave) in the step kernel: its register budget is
+// set by the attention stage, so the matvec stages can hold more groups in
+// flight than the standalone kernel (a Q6_K group takes 40 VGPRs, a Q4_K 24).
+#ifndef RIBN_RING_Q6
+#define RIBN_RING_Q6 3
+#endif
+#ifndef RIBN_RING_Q4
+#define RIBN_RING_Q4 4
+#endif
+template <int T>
+constexpr int step_ring() { return T == 14 ? RIBN_RING_Q6 : RIBN_RING_Q4; }
 
 // Value types of one model's matrices: QKV (q/k, v), attn_output, gate/up,
 // down, head. The step kernel is compiled per profile, head dimension, query
@@ -116,7 +136,9 @@ template <typename PR, int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void step_kernel(StepArgs s) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int wg = blockIdx.x, n_wg = gridDim.x;
-    const GridSync sync{s.bar, (uint32_t)n_wg, (uint64_t)wall_clock64() + s.timeout_ticks};
+    int ns = 0;
+    const GridSync sync{s.bar, (uint32_t)n_wg, (uint64_t)wall_clock64() + s.timeout_ticks,
+                        wg == 0 ? s.stamps : nullptr, &ns};
     const SeqState* seq = s.ctl->seq;
     const int pos = seq->pos;
     const int32_t* pages = seq->pages;
@@ -133,27 +155,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
     uint64_t best = 0ull;
     const int n_splits = splits_for_ctx(pos + 1);
-    uint64_t* const stamp = wg == 0 && threadIdx.x == 0 ? s.stamps : nullptr;
-    int ns = 0;
-    if (stamp) stamp[ns++] = wall_clock64();
+    sync.mark();
     for (int l = 0; l < s.n_layers; l++) {
         const LayerDev& L = s.layers[l];
-        if (!mv_wg<PR::qa, PR::qb, MV_STORE, kRingStep>(L.qkv, wg, lds, best, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
+        if (!mv_wg<PR::qa, PR::qb, MV_STORE, step_ring<PR::qa>(), step_ring<PR::qb>()>(L.qkv, wg, lds, best, sync)) return;
+        sync.mark();
         AttnArgs at = L.attn;
         at.n_splits = n_splits;
         if (!attn_items<HD, G, F16>(at, wg, n_wg, pos, pages, lds, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
-        if (!mv_wg<PR::o, PR::o, MV_ADD, kRingStep>(L.o, wg, lds, best, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
-        if (!mv_wg<PR::gu, PR::gu, MV_SILU, kRingStep>(L.gu, wg, lds, best, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
-        if (!mv_wg<PR::dn, PR::dn, MV_ADD, kRingStep>(L.down, wg, lds, best, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
+        sync.mark();
+        if (!mv_wg<PR::o, PR::o, MV_ADD, step_ring<PR::o>(), step_ring<PR::o>()>(L.o, wg, lds, best, sync)) return;
+        sync.mark();
+        if (!mv_wg<PR::gu, PR::gu, MV_SILU, step_ring<PR::gu>(), step_ring<PR::gu>()>(L.gu, wg, lds, best, sync)) return;
+        sync.mark();
+        if (!mv_wg<PR::dn, PR::dn, MV_ADD, step_ring<PR::dn>(), step_ring<PR::dn>()>(L.down, wg, lds, best, sync)) return;
+        sync.mark();
     }
     if (s.head) {
-        if (!mv_wg<PR::ht, PR::ht, MV_HEAD, kRingStep>(s.head_mv, wg, lds, best, sync)) return;
-        if (stamp) stamp[ns++] = wall_clock64();
+        if (!mv_wg<PR::ht, PR::ht, MV_HEAD, step_ring<PR::ht>(), step_ring<PR::ht>()>(s.head_mv, wg, lds, best, sync)) return;
+        sync.mark();
         head_finish(s.head_mv, best, wg, n_wg);
     } else if (wg == 0 && threadIdx.x == 0) {
         // every workgroup read the position before the first barrier
