@@ -167,6 +167,14 @@ int ribn_rocm_generate(ribn_rocm_model *model, const uint32_t *prompt, uint32_t 
 int ribn_rocm_trace(ribn_rocm_model *model, const uint32_t *tokens, uint32_t n, uint32_t *argmax_out,
                     float *logits_out, float *hidden_out, char *err, size_t err_len);
 
+/* Chunked prefill parity trace: tokens[0..n) through the chunked prefill path
+ * (prefill_chunk / run_prefill_chunk, nvidia/src/decode.rs:2124,2360) in chunks of
+ * min(chunk, prepared) rows (0 = prepared) on a scratch sequence. logits_out
+ * [n][vocab] (final RMSNorm + head for every row) and hidden_out
+ * [(layers + 1)][n][hidden] (after the embedding and every layer) are optional. */
+int ribn_rocm_prefill_trace(ribn_rocm_model *model, const uint32_t *tokens, uint32_t n, uint32_t chunk,
+                            float *logits_out, float *hidden_out, char *err, size_t err_len);
+
 /* ------------------------------------------------------------------------ */
 /* Kernel-level entry points (tests and bench). Host buffers in and out; the
  * weights go through the same load-time re-tiling as model tensors. */
@@ -184,6 +192,11 @@ int ribn_rocm_gemv(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t
  * HIP-event average per launch (on the launch stream). */
 int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, uint32_t iters, double *avg_ms,
                          char *err, size_t err_len);
+/* Y[m][rows] = f16(X)[m][k] * dequantized(W)^T with the prefill MFMA GEMM (the
+ * batched projection of gemv_batch, nvidia/src/decode.rs:1591-1633): X is rounded
+ * to binary16, W dequantized exactly and rounded to binary16, fp32 accumulation. */
+int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t k, const float *x,
+                           uint64_t m, float *y, char *err, size_t err_len);
 /* Greedy argmax (model_ops.rs:203-260): first maximum, NaN skipped. */
 int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, size_t err_len);
 

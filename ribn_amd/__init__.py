@@ -141,6 +141,10 @@ _sig("ribn_rocm_bench_model_kernel", _c.c_int, _c.c_void_p, _c.c_uint32, _c.c_ui
      _c.POINTER(_c.c_uint64), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_step_stamps", _c.c_int, _c.c_void_p, _c.c_uint32, _c.POINTER(_c.c_double), _c.c_size_t,
      _c.POINTER(_c.c_size_t), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_prefill_trace", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _c.c_uint32, _f32p, _f32p, _c.c_char_p,
+     _c.c_size_t)
+_sig("ribn_rocm_prefill_gemm", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _c.c_uint64, _f32p,
+     _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_synth_qwen_gguf", _c.c_int, _c.c_char_p, _c.POINTER(SynthConfig), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_quantize", _c.c_int, _c.c_uint32, _f32p, _c.c_uint64, _u8p)
 
@@ -215,6 +219,18 @@ def bench_gemv(type_: int, rows: int, k: int, iters: int = 50) -> float:
     err = ctypes.create_string_buffer(_ERR)
     _check(_lib.ribn_rocm_bench_gemv(type_, rows, k, iters, ctypes.byref(ms), err, _ERR), err)
     return ms.value
+
+
+def prefill_gemm(type_: int, blocks: np.ndarray, rows: int, k: int, x: np.ndarray) -> np.ndarray:
+    """Y = f16(X) dequant(W)^T with the prefill MFMA GEMM; X is [m][k]."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.shape[0]
+    y = np.empty((m, rows), dtype=np.float32)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_prefill_gemm(type_, _ptr(blocks, _u8p), rows, k, _ptr(x, _f32p), m, _ptr(y, _f32p), err,
+                                       _ERR), err)
+    return y
 
 
 def argmax(logits: np.ndarray) -> int:
@@ -359,6 +375,16 @@ class QwenRocm:
                    None if lg is None else _ptr(lg, _f32p), None if hd is None else _ptr(hd, _f32p))
         return am, lg, hd
 
+    def prefill_trace(self, tokens: Sequence[int], chunk: int = 0, logits: bool = True, hidden: bool = False):
+        """Chunked-prefill trace: (logits [n][vocab], hidden [n][layers + 1][hidden]) per row."""
+        t = _u32(tokens)
+        n = t.size
+        lg = np.zeros((n, self.info.vocab), dtype=np.float32) if logits else None
+        hd = np.zeros((self.info.layers + 1, n, self.info.hidden), dtype=np.float32) if hidden else None
+        self._call(_lib.ribn_rocm_prefill_trace, _ptr(t, _u32p), n, chunk, None if lg is None else _ptr(lg, _f32p),
+                   None if hd is None else _ptr(hd, _f32p))
+        return lg, (None if hd is None else np.ascontiguousarray(hd.transpose(1, 0, 2)))
+
     def step_stamps(self, ctx: int):
         """Wall-clock marks (ns) of one persistent step at context ctx (see ribn_rocm_step_stamps)."""
         cap = 64 * (self.info.layers + 1)
@@ -376,6 +402,6 @@ class QwenRocm:
 
 __all__ = [
     "QwenRocm", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
-    "dequantize", "gemv", "bench_gemv", "argmax", "LIB_PATH", "GGML_F32", "GGML_F16", "GGML_Q8_0", "GGML_Q4_K",
+    "dequantize", "gemv", "bench_gemv", "prefill_gemm", "argmax", "LIB_PATH", "GGML_F32", "GGML_F16", "GGML_Q8_0", "GGML_Q4_K",
     "GGML_Q6_K", "BLOCK", "STEP_PREFILL", "STEP_DECODE", "ADMIT_READY", "ADMIT_REJECTED", "ADMIT_DEFERRED",
 ]

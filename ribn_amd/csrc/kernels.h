@@ -161,6 +161,46 @@ struct StepArgs {
     uint64_t* stamps;          // optional: workgroup 0's wall clock at start and after each stage
 };
 
+// Chunked prefill (prefill.hip). One GEMM: Y[M][col0 + n] (row stride ldy)
+// = X[M][k] deq(W)^T (+ bias[n]) for the N = w.rows weight rows; X is binary16.
+struct PrefillGemm {
+    const uint16_t* x;   // [m][k] binary16
+    int m, k;
+    QMat w;
+    float* y;
+    int ldy, col0;
+    const float* res;    // MV_ADD: y = res + x w^T (res may be y)
+    const float* bias;   // optional [w.rows]
+    int mode;            // MV_STORE or MV_ADD
+};
+
+// Rows of one prefill chunk at positions pos0 .. pos0 + m - 1.
+struct PrefillRows {
+    const float* qkv;    // [m][ld_qkv]: q | k | v projections
+    int ld_qkv;
+    float* qout;         // [m][hq * hd] q after norm and rope
+    uint16_t* attn16;    // [m][hq * hd] attention output, binary16
+    int m, pos0;
+    int hq, hkv, hd, rot, kv_f16;
+    const float* q_norm;
+    const float* k_norm;
+    const float* inv_freq;
+    float eps;
+    const int32_t* pages;
+    uint16_t* kcache;
+    uint16_t* vcache;
+};
+
+size_t prefill_gemm_lds_bytes();
+hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t stream);
+hipError_t launch_rows_rms_f16(const float* x, int m, int k, const float* w, float eps, bool norm, uint16_t* out,
+                               int ldo, hipStream_t stream);
+hipError_t launch_embed_rows(const QMat& w, const uint32_t* tokens, int m, int hidden, float* h, hipStream_t stream);
+hipError_t launch_qk_rope_append(const PrefillRows& p, hipStream_t stream);
+hipError_t launch_prefill_attention(const PrefillRows& p, hipStream_t stream);
+hipError_t launch_silu_mul_f16(const float* gu, int f, int m, uint16_t* act, hipStream_t stream);
+hipError_t launch_set_pos(SeqState* s, int pos, hipStream_t stream);
+
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);
 int matvec_rows_per_wg(const MvArgs& a);

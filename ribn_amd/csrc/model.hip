@@ -102,6 +102,11 @@ struct ribn_rocm_model {
     MvArgs mv_head{};
     std::map<int, hipGraphExec_t> graphs;   // key: n_splits * 2 + head
 
+    // chunked prefill buffers (prefill.hip), rows per chunk = chunk
+    int chunk = 0;
+    float *p_h = nullptr, *p_qkv = nullptr, *p_q = nullptr, *p_gu = nullptr;
+    uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
+
     // persistent step (one launch per token); step_wg == 0: launch chain only
     int step_wg = 0;
     size_t step_lds = 0;
@@ -579,6 +584,80 @@ hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
     return hipGraphLaunch(it->second, M->stream);
 }
 
+// One prefill chunk of the sequence in `slot`: rows pos0 .. pos0 + m - 1 of its
+// token array through every layer (prefill_chunk, nvidia/src/decode.rs:2124).
+// final: the last row's hidden state goes through the head and its greedy
+// token is written at pos0 + m (sampled-final, decode.rs:807-840); else the
+// position just advances. trace (device, optional): hidden rows after the
+// embedding and after every layer, [(L + 1)][m][hidden].
+hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool final, float* trace) {
+    hipStream_t st = M->stream;
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd, ldq = qd + 2 * kd;
+    const uint32_t* toks = M->d_tokens + (size_t)slot * (M->context + 1) + pos0;
+    hipError_t e = launch_embed_rows(M->embd, toks, m, M->H, M->p_h, st);
+    if (e != hipSuccess) return e;
+    auto snap = [&](int i) {
+        return trace ? hipMemcpyAsync(trace + (size_t)i * m * M->H, M->p_h, sizeof(float) * m * M->H,
+                                      hipMemcpyDeviceToDevice, st)
+                     : hipSuccess;
+    };
+    if ((e = snap(0)) != hipSuccess) return e;
+    PrefillRows rows{};
+    rows.qkv = M->p_qkv;
+    rows.ld_qkv = ldq;
+    rows.qout = M->p_q;
+    rows.attn16 = M->p_att16;
+    rows.m = m;
+    rows.pos0 = pos0;
+    rows.hq = M->hq; rows.hkv = M->hkv; rows.hd = M->hd; rows.rot = M->rot;
+    rows.kv_f16 = M->kv_f16 ? 1 : 0;
+    rows.inv_freq = M->inv_freq;
+    rows.eps = M->eps;
+    rows.pages = M->d_pages + (size_t)slot * M->max_pages;
+    auto gemm = [&](const uint16_t* x, int k, const QMat& w, float* y, int ldy, int col0, const float* bias, int mode) {
+        PrefillGemm g{};
+        g.x = x; g.m = m; g.k = k; g.w = w; g.y = y; g.ldy = ldy; g.col0 = col0; g.res = y; g.bias = bias; g.mode = mode;
+        return launch_prefill_gemm(g, st);
+    };
+    for (int l = 0; l < M->L; l++) {
+        const Layer& y = M->layers[l];
+        if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, y.q, M->p_qkv, ldq, 0, y.q_bias, MV_STORE)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, y.k, M->p_qkv, ldq, qd, y.k_bias, MV_STORE)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, y.v, M->p_qkv, ldq, qd + kd, y.v_bias, MV_STORE)) != hipSuccess) return e;
+        rows.q_norm = y.q_norm;
+        rows.k_norm = y.k_norm;
+        rows.kcache = y.kc;
+        rows.vcache = y.vc;
+        if ((e = launch_qk_rope_append(rows, st)) != hipSuccess) return e;
+        if ((e = launch_prefill_attention(rows, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_att16, qd, y.o, M->p_h, M->H, 0, nullptr, MV_ADD)) != hipSuccess) return e;
+        if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.ffn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, y.gate, M->p_gu, 2 * M->F, 0, nullptr, MV_STORE)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, y.up, M->p_gu, 2 * M->F, M->F, nullptr, MV_STORE)) != hipSuccess) return e;
+        if ((e = launch_silu_mul_f16(M->p_gu, M->F, m, M->p_act16, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_act16, M->F, y.down, M->p_h, M->H, 0, nullptr, MV_ADD)) != hipSuccess) return e;
+        if ((e = snap(l + 1)) != hipSuccess) return e;
+    }
+    SeqState* seq = &M->d_slots[slot];
+    if (!final) return launch_set_pos(seq, pos0 + m, st);
+    e = hipMemcpyAsync(M->h, M->p_h + (size_t)(m - 1) * M->H, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = launch_set_pos(seq, pos0 + m - 1, st);
+    if (e == hipSuccess) e = launch_matvec(M->mv_head, M->head_wgs, st);
+    return e;
+}
+
+// Prompt rows pos0 .. pos0 + n - 1 of the sequence in `slot` in chunks of at
+// most M->chunk rows; the last chunk samples the next token when `final`.
+hipError_t prefill_rows(ribn_rocm_model* M, int slot, int pos0, int n, bool final) {
+    for (int p = 0; p < n; p += M->chunk) {
+        const int m = std::min(M->chunk, n - p);
+        hipError_t e = prefill_chunk(M, slot, pos0 + p, m, final && p + m == n, nullptr);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 // One token step of the active sequence: the persistent step kernel when the
 // model has one, else the launch chain (graph replay; eager when tracing).
 // trace (device, (L+1) x hidden): residual stream after the embedding and
@@ -838,6 +917,18 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(dalloc(M, &M->counters, sizeof(uint32_t) * n_counters));
     HIPCHK(hipMemsetAsync(M->counters, 0, sizeof(uint32_t) * n_counters, M->stream));
     HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * std::max<size_t>((size_t)M->V / 2 + 64, 8192)));
+    {
+        M->chunk = (int)std::min<uint32_t>(M->max_batch_tokens, 512);
+        const size_t c = (size_t)M->chunk;
+        const size_t kmax = (size_t)std::max(std::max(M->H, M->F), qd);
+        HIPCHK(dalloc(M, &M->p_h, sizeof(float) * c * M->H));
+        HIPCHK(dalloc(M, &M->p_qkv, sizeof(float) * c * (qd + 2 * kd)));
+        HIPCHK(dalloc(M, &M->p_q, sizeof(float) * c * qd));
+        HIPCHK(dalloc(M, &M->p_gu, sizeof(float) * c * 2 * M->F));
+        HIPCHK(dalloc(M, &M->p_x16, 2 * c * kmax));
+        HIPCHK(dalloc(M, &M->p_att16, 2 * c * qd));
+        HIPCHK(dalloc(M, &M->p_act16, 2 * c * M->F));
+    }
 
     const int slots = (int)M->max_seqs + 1;
     HIPCHK(dalloc(M, &M->d_slots, sizeof(SeqState) * slots));
@@ -930,8 +1021,7 @@ extern "C" int ribn_rocm_generate(ribn_rocm_model* M, const uint32_t* prompt, ui
     if (e == hipSuccess) e = reset_slot(M, slot, pages, prompt, n_prompt);
     if (e == hipSuccess) e = select_slot(M, slot);
     if (e == hipSuccess) e = hipEventRecord(e0, M->stream);
-    for (uint32_t p = 0; e == hipSuccess && p + 1 < n_prompt; p++) e = run_step(M, false, (int)p + 1, nullptr);
-    if (e == hipSuccess) e = run_step(M, true, (int)n_prompt, nullptr);
+    if (e == hipSuccess) e = prefill_rows(M, slot, 0, (int)n_prompt, true);
     if (e == hipSuccess) e = hipEventRecord(e1, M->stream);
     for (uint32_t t = 1; e == hipSuccess && t < n_new; t++) e = run_step(M, true, (int)(n_prompt + t), nullptr);
     if (e == hipSuccess) e = hipEventRecord(e2, M->stream);
@@ -1126,9 +1216,14 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
         s.in_flight = true;
         e = select_slot(M, s.slot);
         const uint32_t end = it.prefix + it.token_budget;
-        for (uint32_t p = it.prefix; e == hipSuccess && p < end; p++) {
-            const bool head = (p + 1 == end) && it.output_budget > 0;
-            e = run_step(M, head, (int)p + 1, nullptr);
+        if (it.token_budget >= 2) {
+            // prompt rows: chunked prefill (the last chunk samples when the row has an output)
+            if (e == hipSuccess) e = prefill_rows(M, s.slot, (int)it.prefix, (int)it.token_budget, it.output_budget > 0);
+        } else {
+            for (uint32_t p = it.prefix; e == hipSuccess && p < end; p++) {
+                const bool head = (p + 1 == end) && it.output_budget > 0;
+                e = run_step(M, head, (int)p + 1, nullptr);
+            }
         }
         if (e == hipSuccess && it.output_budget > 0)
             e = hipMemcpyAsync(&M->h_out[r], &M->d_slots[s.slot].last_token, 4, hipMemcpyDeviceToHost, M->stream);
@@ -1478,5 +1573,79 @@ extern "C" int ribn_rocm_step_stamps(ribn_rocm_model* M, uint32_t ctx, double* o
     while (m < count && h[m] != 0) m++;
     for (size_t i = 0; i < m; i++) out_ns[i] = (double)(h[i] - h[0]) * 1e6 / (double)khz;
     *n = m;
+    return RIBN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Chunked-prefill parity entry points.
+
+// Runs tokens[0..n) through chunked prefill (chunks of min(chunk, prepared)
+// rows) on the scratch sequence; logits_out [n][vocab] of every row (final
+// RMSNorm + head, same GEMM path) and hidden_out [(layers + 1)][n][hidden]
+// (after the embedding and after every layer), both optional.
+extern "C" int ribn_rocm_prefill_trace(ribn_rocm_model* M, const uint32_t* tokens, uint32_t n, uint32_t chunk,
+                                       float* logits_out, float* hidden_out, char* err, size_t err_len) {
+    if (!M || !tokens) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
+    if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    if (n == 0 || n + 1 > M->context) return fail(nullptr, err, err_len, "trace length outside the context", RIBN_ERR_INVALID);
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
+    const int c = (int)std::max<uint32_t>(1, std::min<uint32_t>(chunk ? chunk : M->chunk, (uint32_t)M->chunk));
+    std::vector<int32_t> pages;
+    if (!take_pages(M, n + 1, &pages)) return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
+    const int slot = (int)M->max_seqs;
+    float *dtrace = nullptr, *dlog = nullptr;
+    hipError_t e = hipMalloc(&dtrace, sizeof(float) * (size_t)(M->L + 1) * c * M->H);
+    if (e == hipSuccess && logits_out) e = hipMalloc(&dlog, sizeof(float) * (size_t)c * M->V);
+    if (e == hipSuccess) e = reset_slot(M, slot, pages, tokens, n);
+    if (e == hipSuccess) e = select_slot(M, slot);
+    for (uint32_t p0 = 0; e == hipSuccess && p0 < n; p0 += c) {
+        const int m = (int)std::min<uint32_t>(c, n - p0);
+        e = prefill_chunk(M, slot, (int)p0, m, false, dtrace);
+        if (e == hipSuccess && logits_out) {
+            e = launch_rows_rms_f16(M->p_h, m, M->H, M->out_norm, M->eps, true, M->p_x16, M->H, M->stream);
+            PrefillGemm g{};
+            g.x = M->p_x16; g.m = m; g.k = M->H; g.w = M->out; g.y = dlog; g.ldy = M->V; g.mode = MV_STORE;
+            if (e == hipSuccess) e = launch_prefill_gemm(g, M->stream);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(logits_out + (size_t)p0 * M->V, dlog, sizeof(float) * m * M->V, hipMemcpyDeviceToHost,
+                                   M->stream);
+        }
+        for (int l = 0; e == hipSuccess && hidden_out && l <= M->L; l++)
+            e = hipMemcpyAsync(hidden_out + ((size_t)l * n + p0) * M->H, dtrace + (size_t)l * m * M->H,
+                               sizeof(float) * m * M->H, hipMemcpyDeviceToHost, M->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(M->stream);
+    }
+    if (dtrace) hipFree(dtrace);
+    if (dlog) hipFree(dlog);
+    give_pages(M, pages);
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("prefill trace", e));
+    return RIBN_OK;
+}
+
+// Y[m][rows] = f16(X)[m][k] deq(W)^T with the prefill GEMM (X rounded to binary16
+// on the device, W re-tiled like model tensors).
+extern "C" int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t k, const float* x,
+                                      uint64_t m, float* y, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string msg = check_shape(type, rows, k);
+    if (!msg.empty() || !blocks || !x || !y || m == 0)
+        return fail(nullptr, err, err_len, msg.empty() ? "null argument" : msg, RIBN_ERR_INVALID);
+    if (type != GGML_Q8_0 && k % 256) return fail(nullptr, err, err_len, "k must be a multiple of 256", RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    float *dx = nullptr, *dy = nullptr;
+    uint16_t* dx16 = nullptr;
+    HIPCHK(upload_plain(S, type, rows, k, blocks, &q));
+    HIPCHK(S.alloc(&dx, sizeof(float) * m * k));
+    HIPCHK(S.alloc(&dy, sizeof(float) * m * rows));
+    HIPCHK(S.alloc(&dx16, 2 * m * k));
+    HIPCHK(hipMemcpy(dx, x, sizeof(float) * m * k, hipMemcpyHostToDevice));
+    HIPCHK(launch_rows_rms_f16(dx, (int)m, (int)k, nullptr, 0.f, false, dx16, (int)k, nullptr));
+    PrefillGemm g{};
+    g.x = dx16; g.m = (int)m; g.k = (int)k; g.w = q; g.y = dy; g.ldy = (int)rows; g.mode = MV_STORE;
+    HIPCHK(launch_prefill_gemm(g, nullptr));
+    HIPCHK(hipMemcpy(y, dy, sizeof(float) * m * rows, hipMemcpyDeviceToHost));
     return RIBN_OK;
 }

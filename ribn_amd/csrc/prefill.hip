@@ -1,0 +1,541 @@
+// Chunked prefill: the prompt's rows run through every layer together, so each
+// weight matrix is read once per chunk and the projections are dense GEMMs on
+// the matrix cores (prefill_chunk / run_prefill_chunk, nvidia/src/decode.rs:2124,
+// 2360; the reference batches 8 rows through warp GEMVs, this build uses MFMA).
+//
+//  * prefill_gemm: Y[M][N] = X[M][K] deq(W)^T. X is binary16 (the RMSNorm'd or
+//    activation rows), W stays in its GGUF planes and each 256-wide K slice of a
+//    128-row tile is dequantized (exactly as dequantize_block, then rounded to
+//    binary16) into LDS; v_mfma_f32_16x16x32_f16 accumulates in fp32.
+//  * rows_rms_f16, embed_rows, qk_rope_append, prefill_attention, silu_mul_f16:
+//    the per-row steps around the GEMMs, same equations as the decode kernels.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include "kernels.h"
+
+namespace ribn {
+namespace {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u4v_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kTileM = 128;   // chunk rows per workgroup
+constexpr int kTileN = 128;   // weight rows per workgroup
+constexpr int kTileK = 256;   // one Q4_K / Q6_K super-block, eight Q8_0 blocks
+constexpr int kLdsRow = kTileK + 8;   // halves per LDS row (16-byte pad against bank conflicts)
+
+__device__ __forceinline__ float h2f_bits(uint32_t b) { return __half2float(__ushort_as_half((unsigned short)(b & 0xffffu))); }
+__device__ __forceinline__ float canon(uint32_t b) {
+    const float v = h2f_bits(b);
+    return v != v ? __uint_as_float(0x7fc00000u) : v;
+}
+__device__ __forceinline__ uint16_t f2h_bits(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Dequantize half of one super-block row slice (128 values, exact fp32 as
+// dequantize_block, gguf/src/lib.rs:584-649) into LDS as binary16.
+template <int T>
+__device__ __forceinline__ void deq_half(const QMat& w, size_t row, int blk, int half, uint16_t* dst);
+
+template <>
+__device__ __forceinline__ void deq_half<12>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
+    const size_t bi = row * w.nb + blk;
+    const uint32_t dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
+    const float d = canon(dd), dmin = canon(dd >> 16);
+    const uint32_t* sc = reinterpret_cast<const uint32_t*>(w.b + bi * 16);
+    const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * half);
+#pragma unroll
+    for (int pp = 0; pp < 2; pp++) {   // group pair p = 2 half + pp: groups 2p (low nibbles), 2p+1 (high)
+        const uint32_t s = sc[2 * half + pp];   // sc(2p), sc(2p+1), m(2p), m(2p+1)
+        const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
+        const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
+        const int g = 2 * pp;   // local group of the half (dst already points at the half)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {   // 16 bytes = 16 values of each group
+            const u4v_t q = qs[2 * pp + c];
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+                uint32_t a0 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)(v & 15u)), m0));
+                uint32_t a1 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 8) & 15u)), m0));
+                uint32_t a2 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 16) & 15u)), m0));
+                uint32_t a3 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 24) & 15u)), m0));
+                uint32_t b0 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 4) & 15u)), m1));
+                uint32_t b1 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 12) & 15u)), m1));
+                uint32_t b2 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 20) & 15u)), m1));
+                uint32_t b3 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)(v >> 28)), m1));
+                lo[2 * j] = a0 | (a1 << 16);
+                lo[2 * j + 1] = a2 | (a3 << 16);
+                hi[2 * j] = b0 | (b1 << 16);
+                hi[2 * j + 1] = b2 | (b3 << 16);
+            }
+            u4v_t* o0 = reinterpret_cast<u4v_t*>(dst + g * 32 + 16 * c);
+            u4v_t* o1 = reinterpret_cast<u4v_t*>(dst + (g + 1) * 32 + 16 * c);
+            o0[0] = u4v_t{lo[0], lo[1], lo[2], lo[3]};
+            o0[1] = u4v_t{lo[4], lo[5], lo[6], lo[7]};
+            o1[0] = u4v_t{hi[0], hi[1], hi[2], hi[3]};
+            o1[1] = u4v_t{hi[4], hi[5], hi[6], hi[7]};
+        }
+    }
+}
+
+template <>
+__device__ __forceinline__ void deq_half<14>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
+    // half h = chunk h of 128 values: ql bytes 64h.., qh bytes 32h..; value 32v + l of
+    // the chunk: q = ((ql[32(v%2) + l] >> 4(v/2)) & 15) | (((qh[l] >> 2v) & 3) << 4) - 32,
+    // scale of sub-block 8h + 2v + l/16 (c plane byte 2c + slot, c = 4(s/8) + s%4, slot = (s/4)%2)
+    const size_t bi = row * w.nb + blk;
+    const float d = canon(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
+    const uint8_t* ql = w.a + bi * 128 + 64 * half;
+    const uint8_t* qh = w.b + bi * 64 + 32 * half;
+    const uint8_t* sp = w.c + bi * 16;
+    float gs[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int s = 8 * half + j;
+        gs[j] = __fmul_rn(d, (float)(int8_t)sp[2 * (4 * (s / 8) + s % 4) + (s / 4) % 2]);
+    }
+    const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(ql);
+    const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(qh);
+#pragma unroll
+    for (int lc = 0; lc < 2; lc++) {   // l in [16 lc, 16 lc + 16)
+        const u4v_t qhv = qh4[lc];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const u4v_t qlv = ql4[2 * (v % 2) + lc];
+            uint32_t o[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t lw = j == 0 ? qlv.x : j == 1 ? qlv.y : j == 2 ? qlv.z : qlv.w;
+                const uint32_t hw = j == 0 ? qhv.x : j == 1 ? qhv.y : j == 2 ? qhv.z : qhv.w;
+                uint32_t e[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int q = (int)((((lw >> (8 * b)) >> (4 * (v / 2))) & 15u) |
+                                        ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
+                    e[b] = f2h_bits(__fmul_rn(gs[2 * v + lc], (float)q));
+                }
+                o[2 * j] = e[0] | (e[1] << 16);
+                o[2 * j + 1] = e[2] | (e[3] << 16);
+            }
+            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * v + 16 * lc);
+            out[0] = u4v_t{o[0], o[1], o[2], o[3]};
+            out[1] = u4v_t{o[4], o[5], o[6], o[7]};
+        }
+    }
+}
+
+template <>
+__device__ __forceinline__ void deq_half<8>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
+    // 256-wide slice = Q8_0 blocks 8 blk .. 8 blk + 7; half = blocks 4 half .. +3
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int qb = blk * 8 + 4 * half + b;   // past the row's end (k % 256 != 0): zeros
+        if (qb >= (int)w.nb) {
+            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * b);
+            out[0] = out[1] = out[2] = out[3] = u4v_t{0u, 0u, 0u, 0u};
+            continue;
+        }
+        const size_t bi = row * w.nb + (size_t)qb;
+        const float d = canon(*reinterpret_cast<const uint16_t*>(w.b + bi * 2));
+        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const u4v_t q = qs[c];
+            uint32_t o[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+                uint32_t e[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) e[k] = f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k))));
+                o[2 * j] = e[0] | (e[1] << 16);
+                o[2 * j + 1] = e[2] | (e[3] << 16);
+            }
+            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * b + 16 * c);
+            out[0] = u4v_t{o[0], o[1], o[2], o[3]};
+            out[1] = u4v_t{o[4], o[5], o[6], o[7]};
+        }
+    }
+}
+
+// Workgroup tile: 128 chunk rows x 128 weight rows; wave w owns weight rows
+// 32w..32w+31 of the tile (two 16-column MFMA blocks) for all 128 chunk rows
+// (eight 16-row blocks): 16 accumulators of 4 floats.
+// MFMA 16x16x32 f16 operand layout (lane l): A[m = l%16][k = 8(l/16) .. +8],
+// B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
+template <int T>
+__global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t plds[];
+    uint16_t* xs = plds;                       // [kTileM][kLdsRow]
+    uint16_t* ws = plds + kTileM * kLdsRow;    // [kTileN][kLdsRow]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
+    const int n_rows = (int)g.w.rows;
+    f4_t acc[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc[i][0] = f4_t{0.f, 0.f, 0.f, 0.f};
+        acc[i][1] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    const int n_k = (g.k + kTileK - 1) / kTileK;
+    for (int kt = 0; kt < n_k; kt++) {
+        __syncthreads();
+        // X slice: 128 rows x 256 halves = 4096 16-byte chunks, 16 per thread
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int idx = j * kGemmThreads + tid;
+            const int r = idx >> 5, c = idx & 31;
+            u4v_t v = u4v_t{0u, 0u, 0u, 0u};
+            const int col = kt * kTileK + c * 8;
+            if (m0 + r < g.m && col < g.k) v = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
+            *reinterpret_cast<u4v_t*>(xs + r * kLdsRow + c * 8) = v;
+        }
+        // W slice: 128 rows x 256, two threads per row (one half each)
+        {
+            const int r = tid >> 1, half = tid & 1;
+            const int row = min(n0 + r, n_rows - 1);
+            deq_half<T>(g.w, (size_t)row, kt, half, ws + r * kLdsRow + 128 * half);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kTileK / 32; ks++) {
+            const int kk = ks * 32 + 8 * (lane >> 4);
+            h8_t b[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; nb++)
+                b[nb] = *reinterpret_cast<const h8_t*>(ws + (32 * wave + 16 * nb + (lane & 15)) * kLdsRow + kk);
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++) {
+                const h8_t a = *reinterpret_cast<const h8_t*>(xs + (16 * mb + (lane & 15)) * kLdsRow + kk);
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[0], acc[mb][0], 0, 0, 0);
+                acc[mb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[1], acc[mb][1], 0, 0, 0);
+            }
+        }
+    }
+    // epilogue: C[m][n] of block (mb, nb): m = 16 mb + 4 (lane / 16) + i, n = 16 nb + lane % 16
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+        const int n = n0 + 32 * wave + 16 * nb + (lane & 15);
+        if (n >= n_rows) continue;
+        const float bias = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * mb + 4 * (lane >> 4) + i;
+                if (m >= g.m) continue;
+                const float v = (i == 0 ? acc[mb][nb].x : i == 1 ? acc[mb][nb].y : i == 2 ? acc[mb][nb].z : acc[mb][nb].w) + bias;
+                float* dst = g.y + (size_t)m * g.ldy + g.col0 + n;
+                if (g.mode == MV_ADD) *dst = g.res[(size_t)m * g.ldy + g.col0 + n] + v;
+                else *dst = v;
+            }
+        }
+    }
+}
+
+// rows x[m][k] -> f16(rms_norm(x) * w) (rms_norm, model_ops.rs:108-157); w may be null
+// (plain conversion). One workgroup per row.
+__global__ __launch_bounds__(256) void rows_rms_f16_kernel(const float* x, int k, const float* w, float eps, int norm,
+                                                           uint16_t* out, int ldo) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (size_t)r * k;
+    float inv = 1.0f;
+    if (norm) {
+        float ss = 0.f;
+        for (int i = tid; i < k; i += 256) ss += xr[i] * xr[i];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = red[0] + red[1] + red[2] + red[3];
+        inv = 1.0f / sqrtf(ss / (float)k + eps);
+    }
+    for (int i = tid; i < k; i += 256) {
+        const float v = w ? xr[i] * inv * w[i] : xr[i] * inv;
+        out[(size_t)r * ldo + i] = f2h_bits(v);
+    }
+}
+
+// token rows: h[r][e] = dequantized token_embd row of tokens[r] (q4_k_embedding)
+__global__ __launch_bounds__(256) void embed_rows_kernel(QMat w, const uint32_t* tokens, int hidden, float* h) {
+    const int r = blockIdx.y;
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= hidden) return;
+    const uint32_t tok = tokens[r];
+    // same exact element dequantization as the decode embedding
+    const size_t nb = w.nb;
+    const uint32_t be = w.type == 8 ? 32u : 256u;
+    const uint32_t blk = (uint32_t)e / be, i = (uint32_t)e % be;
+    const size_t bi = (size_t)tok * nb + blk;
+    float v;
+    if (w.type == 8) {
+        v = __fmul_rn(canon(*reinterpret_cast<const uint16_t*>(w.b + bi * 2)), (float)(int8_t)w.a[bi * 32 + i]);
+    } else if (w.type == 12) {
+        const uint8_t* dd = w.c + bi * 4;
+        const float d = canon(dd[0] | (dd[1] << 8)), dmin = canon(dd[2] | (dd[3] << 8));
+        const uint32_t g = i / 32, j = i % 32;
+        const uint8_t* sp = w.b + bi * 16 + (g / 2) * 4;
+        const uint32_t sc = sp[g % 2], mn = sp[2 + g % 2];
+        const uint32_t q = (w.a[bi * 128 + (g / 2) * 32 + j] >> ((g % 2) * 4)) & 15u;
+        v = __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), (float)q), __fmul_rn(dmin, (float)mn));
+    } else {
+        const uint32_t g = i / 32, pos = i % 32, chunk = g / 4, variant = g % 4;
+        const uint32_t lo = (w.a[bi * 128 + chunk * 64 + (variant % 2) * 32 + pos] >> (variant < 2 ? 0 : 4)) & 15u;
+        const uint32_t hi = (w.b[bi * 64 + chunk * 32 + pos] >> (2 * variant)) & 3u;
+        const float d = canon(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
+        const uint32_t sidx = g * 2 + pos / 16;
+        const int8_t sc = (int8_t)w.c[bi * 16 + 2 * (4 * (sidx / 8) + sidx % 4) + (sidx / 4) % 2];
+        v = __fmul_rn(__fmul_rn(d, (float)sc), (float)((int)(lo | (hi << 4)) - 32));
+    }
+    h[(size_t)r * hidden + e] = v;
+}
+
+// Per row and head: q/k RMSNorm (qwen_reference.rs:382-400), NeoX rope at the
+// row's position (theta = pos * inv_freq, as the decode table), K/V append to
+// the paged cache (kv_append_f16, model_ops.rs:1258-1276). q goes to qout (fp32,
+// for the attention); one workgroup of 64 threads per (row, head), heads
+// 0..hq-1 are q heads, hq..hq+hkv-1 the k/v heads.
+__global__ __launch_bounds__(64) void qk_rope_append_kernel(PrefillRows p) {
+    __shared__ float v[128];
+    const int r = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+    const int hd = p.hd, qd = p.hq * hd, kd = p.hkv * hd;
+    const int pos = p.pos0 + r;
+    const bool is_q = head < p.hq;
+    const int kvh = head - p.hq;
+    const float* src = p.qkv + (size_t)r * p.ld_qkv + (is_q ? head * hd : qd + kvh * hd);
+    for (int d = lane; d < hd; d += 64) v[d] = src[d];
+    __syncthreads();
+    const float* nw = is_q ? p.q_norm : p.k_norm;
+    if (nw) {
+        float ss = 0.f;
+        for (int d = lane; d < hd; d += 64) ss += v[d] * v[d];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + p.eps);
+        __syncthreads();
+        for (int d = lane; d < hd; d += 64) v[d] = v[d] * inv * nw[d];
+        __syncthreads();
+    }
+    const int half = p.rot / 2;
+    float outv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int d = lane + 64 * j;
+        outv[j] = d < hd ? v[d] : 0.f;
+        if (d < 2 * half) {
+            const int pp = d < half ? d : d - half;
+            const float theta = (float)pos * p.inv_freq[pp];
+            const float c = cosf(theta), sn = sinf(theta);
+            outv[j] = d < half ? v[d] * c - v[d + half] * sn : v[d - half] * sn + v[d] * c;
+        }
+    }
+    if (is_q) {
+        for (int j = 0; j < 2; j++) {
+            const int d = lane + 64 * j;
+            if (d < hd) p.qout[(size_t)r * qd + head * hd + d] = outv[j];
+        }
+        return;
+    }
+    const int page = p.pages[pos / kPageTokens];
+    const size_t base = ((size_t)(page * p.hkv + kvh) * kPageTokens + pos % kPageTokens) * hd;
+    const float* vsrc = p.qkv + (size_t)r * p.ld_qkv + qd + kd + kvh * hd;
+    for (int j = 0; j < 2; j++) {
+        const int d = lane + 64 * j;
+        if (d >= hd) continue;
+        const float kv = outv[j], vv = vsrc[d];
+        if (p.kv_f16) {
+            p.kcache[base + d] = f2h_bits(kv);
+            p.vcache[base + d] = f2h_bits(vv);
+        } else {
+            uint32_t ku = __float_as_uint(kv), vu = __float_as_uint(vv);
+            ku = (ku & 0x7fffffffu) > 0x7f800000u ? (ku >> 16) | 0x40u : (ku + 0x7fffu + ((ku >> 16) & 1u)) >> 16;
+            vu = (vu & 0x7fffffffu) > 0x7f800000u ? (vu >> 16) | 0x40u : (vu + 0x7fffu + ((vu >> 16) & 1u)) >> 16;
+            p.kcache[base + d] = (uint16_t)ku;
+            p.vcache[base + d] = (uint16_t)vu;
+        }
+    }
+}
+
+__device__ __forceinline__ float kv_val(uint16_t b, int f16) {
+    return f16 ? __half2float(__ushort_as_half(b)) : __uint_as_float((uint32_t)b << 16);
+}
+
+// Causal attention of a chunk's rows over the paged cache (positions 0 .. own
+// position; attn_score_gqa_paged rows > 1, model_ops.rs:442-554). Workgroup =
+// 16 chunk rows x the G query heads of one KV head; TP threads per (row, head)
+// pair split head_dim; keys in tiles of 32 with an fp32 online softmax.
+constexpr int kAttRows = 16;
+constexpr int kAttKeys = 32;
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
+    constexpr int PAIRS = kAttRows * G;
+    constexpr int TP0 = 256 / PAIRS;
+    constexpr int TP = TP0 >= 16 ? 16 : TP0 >= 8 ? 8 : TP0 >= 4 ? 4 : TP0 >= 2 ? 2 : 1;
+    constexpr int DPT = HD / TP;   // dims per thread
+    __shared__ __attribute__((aligned(16))) uint16_t kt[kAttKeys][HD];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kAttKeys][HD];
+    const int tid = threadIdx.x;
+    const int pair = tid / TP, part = tid % TP;
+    const bool active = pair < PAIRS;
+    const int rr = pair / G, g = pair % G;
+    const int kvh = blockIdx.y;
+    const int r = blockIdx.x * kAttRows + rr;
+    const bool row_ok = active && r < p.m;
+    const int qpos = p.pos0 + r;
+    const int last_pos = p.pos0 + min(p.m - 1, blockIdx.x * kAttRows + kAttRows - 1);
+    const float scale = 1.0f / sqrtf((float)HD);
+    float q[DPT], o[DPT];
+    const int qh = kvh * G + g;
+#pragma unroll
+    for (int i = 0; i < DPT; i++) {
+        q[i] = row_ok ? p.qout[(size_t)r * p.hq * HD + qh * HD + part * DPT + i] * scale : 0.f;
+        o[i] = 0.f;
+    }
+    float mx = -INFINITY, l = 0.f;
+    for (int t0 = 0; t0 <= last_pos; t0 += kAttKeys) {
+        __syncthreads();
+        for (int idx = tid; idx < kAttKeys * HD / 8; idx += 256) {
+            const int t = idx / (HD / 8), c = idx % (HD / 8);
+            const int pos = t0 + t;
+            u4v_t kv = u4v_t{0u, 0u, 0u, 0u}, vv = u4v_t{0u, 0u, 0u, 0u};
+            if (pos <= last_pos) {
+                const int page = p.pages[pos / kPageTokens];
+                const size_t off = ((size_t)(page * p.hkv + kvh) * kPageTokens + pos % kPageTokens) * HD + c * 8;
+                kv = *reinterpret_cast<const u4v_t*>(p.kcache + off);
+                vv = *reinterpret_cast<const u4v_t*>(p.vcache + off);
+            }
+            *reinterpret_cast<u4v_t*>(&kt[t][c * 8]) = kv;
+            *reinterpret_cast<u4v_t*>(&vt[t][c * 8]) = vv;
+        }
+        __syncthreads();
+        float s[kAttKeys];
+#pragma unroll
+        for (int t = 0; t < kAttKeys; t++) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < DPT; i++) a = fmaf(q[i], kv_val(kt[t][part * DPT + i], p.kv_f16), a);
+#pragma unroll
+            for (int o2 = 1; o2 < TP; o2 <<= 1) a += __shfl_xor(a, o2);
+            s[t] = (t0 + t <= qpos) ? a : -INFINITY;
+        }
+        float tm = mx;
+#pragma unroll
+        for (int t = 0; t < kAttKeys; t++) tm = fmaxf(tm, s[t]);
+        if (tm == -INFINITY) continue;   // no visible key in this tile for this row (uniform per pair)
+        const float corr = expf(mx - tm);
+        l *= corr;
+#pragma unroll
+        for (int i = 0; i < DPT; i++) o[i] *= corr;
+#pragma unroll
+        for (int t = 0; t < kAttKeys; t++) {
+            const float pt = expf(s[t] - tm);
+            l += pt;
+#pragma unroll
+            for (int i = 0; i < DPT; i++) o[i] = fmaf(pt, kv_val(vt[t][part * DPT + i], p.kv_f16), o[i]);
+        }
+        mx = tm;
+    }
+    if (!row_ok) return;
+    const float il = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < DPT; i++)
+        p.attn16[(size_t)r * p.hq * HD + qh * HD + part * DPT + i] = f2h_bits(o[i] * il);
+}
+
+// act16[r][j] = f16(silu(gu[r][j]) * gu[r][F + j]) (silu_mul, model_ops.rs:318-330)
+__global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* gu, int f, int m, uint16_t* act) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)m * f) return;
+    const size_t r = i / f, j = i % f;
+    const float g = gu[r * 2 * f + j], u = gu[r * 2 * f + f + j];
+    act[i] = f2h_bits(g / (1.0f + expf(-g)) * u);
+}
+
+__global__ void set_pos_kernel(SeqState* s, int pos) {
+    if (threadIdx.x == 0) s->pos = pos;
+}
+
+template <int HD>
+hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
+    const dim3 grid((p.m + kAttRows - 1) / kAttRows, p.hkv);
+    switch (p.hq / p.hkv) {
+    case 1: prefill_attention_kernel<HD, 1><<<grid, 256, 0, st>>>(p); break;
+    case 2: prefill_attention_kernel<HD, 2><<<grid, 256, 0, st>>>(p); break;
+    case 4: prefill_attention_kernel<HD, 4><<<grid, 256, 0, st>>>(p); break;
+    case 7: prefill_attention_kernel<HD, 7><<<grid, 256, 0, st>>>(p); break;
+    case 8: prefill_attention_kernel<HD, 8><<<grid, 256, 0, st>>>(p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t prefill_gemm_lds_bytes() { return (size_t)(kTileM + kTileN) * kLdsRow * 2; }
+
+hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
+    // K-quant rows are whole 256-value super-blocks; Q8_0 rows may end inside a slice
+    if (g.m <= 0 || g.k <= 0 || g.k % 32 || (g.w.type != 8 && g.k % kTileK) || g.w.k != (uint32_t)g.k ||
+        g.w.rows == 0)
+        return hipErrorInvalidValue;
+    const dim3 grid((g.w.rows + kTileN - 1) / kTileN, (g.m + kTileM - 1) / kTileM);
+    const size_t lds = prefill_gemm_lds_bytes();
+#define RIBN_PG(T)                                                                                              \
+    {                                                                                                           \
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<T>),              \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);               \
+        if (e != hipSuccess) return e;                                                                          \
+        prefill_gemm_kernel<T><<<grid, kGemmThreads, lds, st>>>(g);                                             \
+        return hipGetLastError();                                                                               \
+    }
+    if (g.w.type == 12) RIBN_PG(12)
+    if (g.w.type == 14) RIBN_PG(14)
+    if (g.w.type == 8) RIBN_PG(8)
+#undef RIBN_PG
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_rows_rms_f16(const float* x, int m, int k, const float* w, float eps, bool norm, uint16_t* out,
+                               int ldo, hipStream_t st) {
+    if (m <= 0) return hipErrorInvalidValue;
+    rows_rms_f16_kernel<<<m, 256, 0, st>>>(x, k, w, eps, norm ? 1 : 0, out, ldo);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const QMat& w, const uint32_t* tokens, int m, int hidden, float* h, hipStream_t st) {
+    if (m <= 0) return hipErrorInvalidValue;
+    embed_rows_kernel<<<dim3((hidden + 255) / 256, m), 256, 0, st>>>(w, tokens, hidden, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_rope_append(const PrefillRows& p, hipStream_t st) {
+    if (p.m <= 0 || p.hd > 128 || p.rot > p.hd) return hipErrorInvalidValue;
+    qk_rope_append_kernel<<<dim3(p.m, p.hq + p.hkv), 64, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillRows& p, hipStream_t st) {
+    if (p.m <= 0 || p.hq % p.hkv) return hipErrorInvalidValue;
+    if (p.hd == 128) return attention_dispatch_prefill<128>(p, st);
+    if (p.hd == 64) return attention_dispatch_prefill<64>(p, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_silu_mul_f16(const float* gu, int f, int m, uint16_t* act, hipStream_t st) {
+    const size_t n = (size_t)m * f;
+    silu_mul_f16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(gu, f, m, act);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_pos(SeqState* s, int pos, hipStream_t st) {
+    set_pos_kernel<<<1, 64, 0, st>>>(s, pos);
+    return hipGetLastError();
+}
+
+}  // namespace ribn

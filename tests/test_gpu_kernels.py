@@ -158,3 +158,28 @@ def test_argmax_semantics():
         if n > 10:
             l[n // 3] = l[n - 2] = l.max() + 1.0   # tie: lowest index wins
         assert ribn_amd.argmax(l) == orc.argmax(l)
+
+
+@pytest.mark.parametrize("t,rows,k,m", [
+    (12, 300, 4096, 130), (14, 257, 4096, 64), (8, 129, 896, 200), (8, 128, 4864, 17), (14, 64, 12288, 5),
+    (12, 1, 256, 1),
+])
+def test_prefill_gemm_vs_fp64(t, rows, k, m):
+    """Chunked-prefill GEMM (MFMA, binary16 operands, fp32 accumulate) against the fp64 product of the
+    oracle-dequantized weights; partial row/column tiles and a Q8_0 width that is not a multiple of 256."""
+    say(f"prefill gemm t={t} rows={rows} k={k} m={m}")
+    blocks = _quant_matrix(t, rows, k, seed=rows * 3 + k)
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = ribn_amd.prefill_gemm(t, blocks, rows, k, x)
+    be, bb = ribn_amd.BLOCK[t]
+    rb = k // be * bb
+    w = np.stack([orc.dequantize(t, blocks[i * rb:(i + 1) * rb]) for i in range(rows)]).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    say(f"  rel-L2 {rel:.2e}")
+    assert y.shape == (m, rows)
+    assert rel <= MATVEC_TOL
+    # every row on its own is within the bar too (no row-block mixing)
+    per_row = np.linalg.norm(y - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    assert per_row.max() <= 4 * MATVEC_TOL

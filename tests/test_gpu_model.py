@@ -122,6 +122,29 @@ def test_trace_hidden_and_logits(model_paths, name, kv, step):
         assert am[p] == orc.argmax(lg[p])   # the device argmax is the argmax of the device logits
 
 
+@pytest.mark.parametrize("chunk", [0, 16])
+@pytest.mark.parametrize("kv", list(KV_MODES))
+@pytest.mark.parametrize("name", list(MODELS))
+def test_chunked_prefill_hidden_and_logits(model_paths, name, kv, chunk):
+    """Chunked prefill (MFMA GEMMs, causal chunk attention) against the FP32 oracle: hidden rows after every
+    layer and the logits of every row; chunk 16 splits the 40 rows over three chunks, so later chunks attend
+    to cache entries written by earlier ones."""
+    path = model_paths[name]
+    kv_round, tol = KV_MODES[kv]
+    rng = np.random.default_rng(4)
+    tokens = rng.integers(0, MODELS[name]["vocab"], 40).tolist()
+    say(f"prefill trace {name} kv={kv} chunk={chunk}")
+    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=2, kv=kv) as m:
+        lg, hd = m.prefill_trace(tokens, chunk=chunk, logits=True, hidden=True)
+    ref_l, ref_h = _oracle_trace(path, tokens, 128, hidden=True, kv_round=kv_round)
+    for layer in range(ref_h.shape[1]):
+        r = _rel(hd[:, layer], ref_h[:, layer])
+        assert r <= tol, f"layer {layer} hidden rel-L2 {r:.2e}"
+    r = _rel(lg, ref_l)
+    say(f"  logits rel-L2 {r:.2e}")
+    assert r <= tol
+
+
 @pytest.mark.parametrize("step", STEPS)
 @pytest.mark.parametrize("kv", list(KV_MODES))
 def test_long_context_split_k(model_paths, kv, step):
