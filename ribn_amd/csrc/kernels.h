@@ -161,17 +161,25 @@ struct StepArgs {
     uint64_t* stamps;          // optional: workgroup 0's wall clock at start and after each stage
 };
 
-// Chunked prefill (prefill.hip). One GEMM: Y[M][col0 + n] (row stride ldy)
-// = X[M][k] deq(W)^T (+ bias[n]) for the N = w.rows weight rows; X is binary16.
+// Chunked prefill (prefill.hip). One GEMM launch over up to three weight
+// matrices (segments) sharing the input: Y[M][col0 + n] (row stride ldy) =
+// X[M][k] deq(W)^T (+ bias[n]) for the w.rows rows of each segment; X is
+// binary16. Segments 0 and 1 share a value type; tile0 = the segment's first
+// 128-row tile (0, then cumulative).
+struct PrefillSeg {
+    QMat w;
+    int col0, tile0;
+    const float* bias;   // optional [w.rows]
+};
 struct PrefillGemm {
     const uint16_t* x;   // [m][k] binary16
     int m, k;
-    QMat w;
     float* y;
-    int ldy, col0;
+    int ldy;
     const float* res;    // MV_ADD: y = res + x w^T (res may be y)
-    const float* bias;   // optional [w.rows]
     int mode;            // MV_STORE or MV_ADD
+    int nseg;
+    PrefillSeg seg[3];
 };
 
 // Rows of one prefill chunk at positions pos0 .. pos0 + m - 1.

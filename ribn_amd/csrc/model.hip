@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <string>
@@ -614,29 +615,39 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     rows.inv_freq = M->inv_freq;
     rows.eps = M->eps;
     rows.pages = M->d_pages + (size_t)slot * M->max_pages;
-    auto gemm = [&](const uint16_t* x, int k, const QMat& w, float* y, int ldy, int col0, const float* bias, int mode) {
+    // one launch per input: q|k|v, attn_output, gate|up, down
+    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs) {
         PrefillGemm g{};
-        g.x = x; g.m = m; g.k = k; g.w = w; g.y = y; g.ldy = ldy; g.col0 = col0; g.res = y; g.bias = bias; g.mode = mode;
+        g.x = x; g.m = m; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
+        int tiles = 0;
+        for (const PrefillSeg& sg : segs) {
+            g.seg[g.nseg] = sg;
+            g.seg[g.nseg].tile0 = tiles;
+            tiles += (int)((sg.w.rows + 127) / 128);
+            g.nseg++;
+        }
         return launch_prefill_gemm(g, st);
     };
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
         if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, y.q, M->p_qkv, ldq, 0, y.q_bias, MV_STORE)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, y.k, M->p_qkv, ldq, qd, y.k_bias, MV_STORE)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, y.v, M->p_qkv, ldq, qd + kd, y.v_bias, MV_STORE)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
+                      {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
+                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
+            return e;
         rows.q_norm = y.q_norm;
         rows.k_norm = y.k_norm;
         rows.kcache = y.kc;
         rows.vcache = y.vc;
         if ((e = launch_qk_rope_append(rows, st)) != hipSuccess) return e;
         if ((e = launch_prefill_attention(rows, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_att16, qd, y.o, M->p_h, M->H, 0, nullptr, MV_ADD)) != hipSuccess) return e;
+        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}})) != hipSuccess) return e;
         if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.ffn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, y.gate, M->p_gu, 2 * M->F, 0, nullptr, MV_STORE)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, y.up, M->p_gu, 2 * M->F, M->F, nullptr, MV_STORE)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
+                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}})) != hipSuccess)
+            return e;
         if ((e = launch_silu_mul_f16(M->p_gu, M->F, m, M->p_act16, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_act16, M->F, y.down, M->p_h, M->H, 0, nullptr, MV_ADD)) != hipSuccess) return e;
+        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}})) != hipSuccess) return e;
         if ((e = snap(l + 1)) != hipSuccess) return e;
     }
     SeqState* seq = &M->d_slots[slot];
@@ -1606,7 +1617,9 @@ extern "C" int ribn_rocm_prefill_trace(ribn_rocm_model* M, const uint32_t* token
         if (e == hipSuccess && logits_out) {
             e = launch_rows_rms_f16(M->p_h, m, M->H, M->out_norm, M->eps, true, M->p_x16, M->H, M->stream);
             PrefillGemm g{};
-            g.x = M->p_x16; g.m = m; g.k = M->H; g.w = M->out; g.y = dlog; g.ldy = M->V; g.mode = MV_STORE;
+            g.x = M->p_x16; g.m = m; g.k = M->H; g.y = dlog; g.ldy = M->V; g.mode = MV_STORE;
+            g.nseg = 1;
+            g.seg[0].w = M->out;
             if (e == hipSuccess) e = launch_prefill_gemm(g, M->stream);
             if (e == hipSuccess)
                 e = hipMemcpyAsync(logits_out + (size_t)p0 * M->V, dlog, sizeof(float) * m * M->V, hipMemcpyDeviceToHost,
@@ -1644,7 +1657,9 @@ extern "C" int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t* blocks, uint
     HIPCHK(hipMemcpy(dx, x, sizeof(float) * m * k, hipMemcpyHostToDevice));
     HIPCHK(launch_rows_rms_f16(dx, (int)m, (int)k, nullptr, 0.f, false, dx16, (int)k, nullptr));
     PrefillGemm g{};
-    g.x = dx16; g.m = (int)m; g.k = (int)k; g.w = q; g.y = dy; g.ldy = (int)rows; g.mode = MV_STORE;
+    g.x = dx16; g.m = (int)m; g.k = (int)k; g.y = dy; g.ldy = (int)rows; g.mode = MV_STORE;
+    g.nseg = 1;
+    g.seg[0].w = q;
     HIPCHK(launch_prefill_gemm(g, nullptr));
     HIPCHK(hipMemcpy(y, dy, sizeof(float) * m * rows, hipMemcpyDeviceToHost));
     return RIBN_OK;

@@ -24,7 +24,7 @@ typedef unsigned u4v_t __attribute__((ext_vector_type(4)));
 constexpr int kGemmThreads = 256;
 constexpr int kTileM = 128;   // chunk rows per workgroup
 constexpr int kTileN = 128;   // weight rows per workgroup
-constexpr int kTileK = 256;   // one Q4_K / Q6_K super-block, eight Q8_0 blocks
+constexpr int kTileK = 128;   // half a Q4_K / Q6_K super-block, four Q8_0 blocks
 constexpr int kLdsRow = kTileK + 8;   // halves per LDS row (16-byte pad against bank conflicts)
 
 __device__ __forceinline__ float h2f_bits(uint32_t b) { return __half2float(__ushort_as_half((unsigned short)(b & 0xffffu))); }
@@ -34,78 +34,75 @@ __device__ __forceinline__ float canon(uint32_t b) {
 }
 __device__ __forceinline__ uint16_t f2h_bits(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
-// Dequantize half of one super-block row slice (128 values, exact fp32 as
-// dequantize_block, gguf/src/lib.rs:584-649) into LDS as binary16.
+// Dequantize 64 consecutive values of one weight row into LDS as binary16:
+// values [128 kt + 64 q, +64) of the row (kt = 128-wide K tile, q = quarter of
+// it), computed exactly as dequantize_block (gguf/src/lib.rs:584-649) and then
+// rounded to binary16.
 template <int T>
-__device__ __forceinline__ void deq_half(const QMat& w, size_t row, int blk, int half, uint16_t* dst);
+__device__ __forceinline__ void deq_quarter(const QMat& w, size_t row, int kt, int q, uint16_t* dst);
+
+__device__ __forceinline__ void store16(uint16_t* dst, const uint32_t (&o)[8]) {
+    u4v_t* out = reinterpret_cast<u4v_t*>(dst);
+    out[0] = u4v_t{o[0], o[1], o[2], o[3]};
+    out[1] = u4v_t{o[4], o[5], o[6], o[7]};
+}
 
 template <>
-__device__ __forceinline__ void deq_half<12>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
-    const size_t bi = row * w.nb + blk;
+__device__ __forceinline__ void deq_quarter<12>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
+    // group pair p = 2 (kt % 2) + q of block kt / 2: group 2p = low nibbles of qs
+    // bytes 32p..32p+31, group 2p+1 = their high nibbles; scale dword p holds
+    // sc(2p), sc(2p+1), m(2p), m(2p+1)
+    const size_t bi = row * w.nb + (kt >> 1);
+    const int p = 2 * (kt & 1) + q;
     const uint32_t dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
     const float d = canon(dd), dmin = canon(dd >> 16);
-    const uint32_t* sc = reinterpret_cast<const uint32_t*>(w.b + bi * 16);
-    const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * half);
+    const uint32_t s = reinterpret_cast<const uint32_t*>(w.b + bi * 16)[p];
+    const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
+    const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
+    const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p);
 #pragma unroll
-    for (int pp = 0; pp < 2; pp++) {   // group pair p = 2 half + pp: groups 2p (low nibbles), 2p+1 (high)
-        const uint32_t s = sc[2 * half + pp];   // sc(2p), sc(2p+1), m(2p), m(2p+1)
-        const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
-        const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
-        const int g = 2 * pp;   // local group of the half (dst already points at the half)
+    for (int c = 0; c < 2; c++) {
+        const u4v_t qv = qs[c];
+        uint32_t lo[8], hi[8];
 #pragma unroll
-        for (int c = 0; c < 2; c++) {   // 16 bytes = 16 values of each group
-            const u4v_t q = qs[2 * pp + c];
-            uint32_t lo[8], hi[8];
+        for (int j = 0; j < 4; j++) {
+            const uint32_t v = j == 0 ? qv.x : j == 1 ? qv.y : j == 2 ? qv.z : qv.w;
+            uint32_t a[4], bb[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t v = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-                uint32_t a0 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)(v & 15u)), m0));
-                uint32_t a1 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 8) & 15u)), m0));
-                uint32_t a2 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 16) & 15u)), m0));
-                uint32_t a3 = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> 24) & 15u)), m0));
-                uint32_t b0 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 4) & 15u)), m1));
-                uint32_t b1 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 12) & 15u)), m1));
-                uint32_t b2 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> 20) & 15u)), m1));
-                uint32_t b3 = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)(v >> 28)), m1));
-                lo[2 * j] = a0 | (a1 << 16);
-                lo[2 * j + 1] = a2 | (a3 << 16);
-                hi[2 * j] = b0 | (b1 << 16);
-                hi[2 * j + 1] = b2 | (b3 << 16);
+            for (int e = 0; e < 4; e++) {
+                a[e] = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> (8 * e)) & 15u)), m0));
+                bb[e] = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> (8 * e + 4)) & 15u)), m1));
             }
-            u4v_t* o0 = reinterpret_cast<u4v_t*>(dst + g * 32 + 16 * c);
-            u4v_t* o1 = reinterpret_cast<u4v_t*>(dst + (g + 1) * 32 + 16 * c);
-            o0[0] = u4v_t{lo[0], lo[1], lo[2], lo[3]};
-            o0[1] = u4v_t{lo[4], lo[5], lo[6], lo[7]};
-            o1[0] = u4v_t{hi[0], hi[1], hi[2], hi[3]};
-            o1[1] = u4v_t{hi[4], hi[5], hi[6], hi[7]};
+            lo[2 * j] = a[0] | (a[1] << 16);
+            lo[2 * j + 1] = a[2] | (a[3] << 16);
+            hi[2 * j] = bb[0] | (bb[1] << 16);
+            hi[2 * j + 1] = bb[2] | (bb[3] << 16);
         }
+        store16(dst + 16 * c, lo);
+        store16(dst + 32 + 16 * c, hi);
     }
 }
 
 template <>
-__device__ __forceinline__ void deq_half<14>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
-    // half h = chunk h of 128 values: ql bytes 64h.., qh bytes 32h..; value 32v + l of
-    // the chunk: q = ((ql[32(v%2) + l] >> 4(v/2)) & 15) | (((qh[l] >> 2v) & 3) << 4) - 32,
-    // scale of sub-block 8h + 2v + l/16 (c plane byte 2c + slot, c = 4(s/8) + s%4, slot = (s/4)%2)
-    const size_t bi = row * w.nb + blk;
+__device__ __forceinline__ void deq_quarter<14>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
+    // chunk h = kt % 2 of block kt / 2 (ql bytes 64h.., qh bytes 32h..); value
+    // 32v + l of the chunk: ((ql[32 (v%2) + l] >> 4 (v/2)) & 15) | (((qh[l] >> 2v) & 3) << 4),
+    // minus 32, times d * sc(8h + 2v + l/16); the quarter q holds v = 2q, 2q + 1.
+    // Sub-block scale s sits at c-plane byte 2c + slot, c = 4 (s/8) + s%4, slot = (s/4) % 2.
+    const size_t bi = row * w.nb + (kt >> 1);
+    const int h = kt & 1;
     const float d = canon(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
-    const uint8_t* ql = w.a + bi * 128 + 64 * half;
-    const uint8_t* qh = w.b + bi * 64 + 32 * half;
     const uint8_t* sp = w.c + bi * 16;
-    float gs[8];
+    const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * h);
+    const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(w.b + bi * 64 + 32 * h);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int s = 8 * half + j;
-        gs[j] = __fmul_rn(d, (float)(int8_t)sp[2 * (4 * (s / 8) + s % 4) + (s / 4) % 2]);
-    }
-    const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(ql);
-    const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(qh);
+    for (int vv = 0; vv < 2; vv++) {
+        const int v = 2 * q + vv;
 #pragma unroll
-    for (int lc = 0; lc < 2; lc++) {   // l in [16 lc, 16 lc + 16)
-        const u4v_t qhv = qh4[lc];
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const u4v_t qlv = ql4[2 * (v % 2) + lc];
+        for (int lc = 0; lc < 2; lc++) {
+            const int sb = 8 * h + 2 * v + lc;
+            const float gsc = __fmul_rn(d, (float)(int8_t)sp[2 * (4 * (sb / 8) + sb % 4) + (sb / 4) % 2]);
+            const u4v_t qlv = ql4[2 * vv + lc], qhv = qh4[lc];
             uint32_t o[8];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -114,67 +111,71 @@ __device__ __forceinline__ void deq_half<14>(const QMat& w, size_t row, int blk,
                 uint32_t e[4];
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
-                    const int q = (int)((((lw >> (8 * b)) >> (4 * (v / 2))) & 15u) |
-                                        ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
-                    e[b] = f2h_bits(__fmul_rn(gs[2 * v + lc], (float)q));
+                    const int qq = (int)((((lw >> (8 * b)) >> (4 * q)) & 15u) | ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
+                    e[b] = f2h_bits(__fmul_rn(gsc, (float)qq));
                 }
                 o[2 * j] = e[0] | (e[1] << 16);
                 o[2 * j + 1] = e[2] | (e[3] << 16);
             }
-            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * v + 16 * lc);
-            out[0] = u4v_t{o[0], o[1], o[2], o[3]};
-            out[1] = u4v_t{o[4], o[5], o[6], o[7]};
+            store16(dst + 32 * vv + 16 * lc, o);
         }
     }
 }
 
 template <>
-__device__ __forceinline__ void deq_half<8>(const QMat& w, size_t row, int blk, int half, uint16_t* dst) {
-    // 256-wide slice = Q8_0 blocks 8 blk .. 8 blk + 7; half = blocks 4 half .. +3
+__device__ __forceinline__ void deq_quarter<8>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
+    // Q8_0 blocks 4 kt + 2q and 4 kt + 2q + 1; past the row's end (k % 128 != 0): zeros
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const int qb = blk * 8 + 4 * half + b;   // past the row's end (k % 256 != 0): zeros
+    for (int b = 0; b < 2; b++) {
+        const int qb = 4 * kt + 2 * q + b;
+        uint32_t o[2][8];
         if (qb >= (int)w.nb) {
-            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * b);
-            out[0] = out[1] = out[2] = out[3] = u4v_t{0u, 0u, 0u, 0u};
-            continue;
-        }
-        const size_t bi = row * w.nb + (size_t)qb;
-        const float d = canon(*reinterpret_cast<const uint16_t*>(w.b + bi * 2));
-        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const u4v_t q = qs[c];
-            uint32_t o[8];
+            for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t v = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-                uint32_t e[4];
+                for (int j = 0; j < 8; j++) o[c][j] = 0u;
+        } else {
+            const size_t bi = row * w.nb + (size_t)qb;
+            const float d = canon(*reinterpret_cast<const uint16_t*>(w.b + bi * 2));
+            const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
 #pragma unroll
-                for (int k = 0; k < 4; k++) e[k] = f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k))));
-                o[2 * j] = e[0] | (e[1] << 16);
-                o[2 * j + 1] = e[2] | (e[3] << 16);
+            for (int c = 0; c < 2; c++) {
+                const u4v_t qv = qs[c];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t v = j == 0 ? qv.x : j == 1 ? qv.y : j == 2 ? qv.z : qv.w;
+                    uint32_t e[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) e[k] = f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k))));
+                    o[c][2 * j] = e[0] | (e[1] << 16);
+                    o[c][2 * j + 1] = e[2] | (e[3] << 16);
+                }
             }
-            u4v_t* out = reinterpret_cast<u4v_t*>(dst + 32 * b + 16 * c);
-            out[0] = u4v_t{o[0], o[1], o[2], o[3]};
-            out[1] = u4v_t{o[4], o[5], o[6], o[7]};
         }
+        store16(dst + 32 * b, o[0]);
+        store16(dst + 32 * b + 16, o[1]);
     }
 }
 
-// Workgroup tile: 128 chunk rows x 128 weight rows; wave w owns weight rows
-// 32w..32w+31 of the tile (two 16-column MFMA blocks) for all 128 chunk rows
-// (eight 16-row blocks): 16 accumulators of 4 floats.
+// Workgroup tile: 128 chunk rows x 128 weight rows of one segment; wave w owns
+// weight rows 32w..32w+31 of the tile (two 16-column MFMA blocks) for all 128
+// chunk rows (eight 16-row blocks): 16 accumulators of 4 floats. K runs in
+// tiles of 128 (X slice and dequantized W slice in LDS, 70 KB: two workgroups
+// per CU, so one stages while the other multiplies).
 // MFMA 16x16x32 f16 operand layout (lane l): A[m = l%16][k = 8(l/16) .. +8],
 // B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
-template <int T>
+template <int TA, int TB>
 __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
     extern __shared__ __attribute__((aligned(16))) uint16_t plds[];
     uint16_t* xs = plds;                       // [kTileM][kLdsRow]
     uint16_t* ws = plds + kTileM * kLdsRow;    // [kTileN][kLdsRow]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
-    const int n_rows = (int)g.w.rows;
+    int si = 0;
+    if (g.nseg > 1 && (int)blockIdx.x >= g.seg[1].tile0) si = 1;
+    if (g.nseg > 2 && (int)blockIdx.x >= g.seg[2].tile0) si = 2;
+    const PrefillSeg sg = g.seg[si];
+    const int m0 = blockIdx.y * kTileM, n0 = ((int)blockIdx.x - sg.tile0) * kTileN;
+    const int n_rows = (int)sg.w.rows;
     f4_t acc[8][2];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -182,24 +183,22 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
         acc[i][1] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
     const int n_k = (g.k + kTileK - 1) / kTileK;
+    const int wr = tid >> 1, wq = tid & 1;   // dequant: row of the tile, quarter of the K tile
+    const size_t wrow = (size_t)min(n0 + wr, n_rows - 1);
     for (int kt = 0; kt < n_k; kt++) {
         __syncthreads();
-        // X slice: 128 rows x 256 halves = 4096 16-byte chunks, 16 per thread
+        // X slice: 128 rows x 128 halves = 2048 16-byte chunks, 8 per thread
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
+        for (int j = 0; j < 8; j++) {
             const int idx = j * kGemmThreads + tid;
-            const int r = idx >> 5, c = idx & 31;
-            u4v_t v = u4v_t{0u, 0u, 0u, 0u};
+            const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
+            u4v_t v = u4v_t{0u, 0u, 0u, 0u};
             if (m0 + r < g.m && col < g.k) v = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
             *reinterpret_cast<u4v_t*>(xs + r * kLdsRow + c * 8) = v;
         }
-        // W slice: 128 rows x 256, two threads per row (one half each)
-        {
-            const int r = tid >> 1, half = tid & 1;
-            const int row = min(n0 + r, n_rows - 1);
-            deq_half<T>(g.w, (size_t)row, kt, half, ws + r * kLdsRow + 128 * half);
-        }
+        if (si == 2 && TB != TA) deq_quarter<TB>(sg.w, wrow, kt, wq, ws + wr * kLdsRow + 64 * wq);
+        else deq_quarter<TA>(sg.w, wrow, kt, wq, ws + wr * kLdsRow + 64 * wq);
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < kTileK / 32; ks++) {
@@ -221,7 +220,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     for (int nb = 0; nb < 2; nb++) {
         const int n = n0 + 32 * wave + 16 * nb + (lane & 15);
         if (n >= n_rows) continue;
-        const float bias = g.bias ? g.bias[n] : 0.f;
+        const float bias = sg.bias ? sg.bias[n] : 0.f;
 #pragma unroll
         for (int mb = 0; mb < 8; mb++) {
 #pragma unroll
@@ -229,9 +228,9 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
                 const int m = m0 + 16 * mb + 4 * (lane >> 4) + i;
                 if (m >= g.m) continue;
                 const float v = (i == 0 ? acc[mb][nb].x : i == 1 ? acc[mb][nb].y : i == 2 ? acc[mb][nb].z : acc[mb][nb].w) + bias;
-                float* dst = g.y + (size_t)m * g.ldy + g.col0 + n;
-                if (g.mode == MV_ADD) *dst = g.res[(size_t)m * g.ldy + g.col0 + n] + v;
-                else *dst = v;
+                const size_t o = (size_t)m * g.ldy + sg.col0 + n;
+                if (g.mode == MV_ADD) g.y[o] = g.res[o] + v;
+                else g.y[o] = v;
             }
         }
     }
@@ -480,23 +479,29 @@ hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
 size_t prefill_gemm_lds_bytes() { return (size_t)(kTileM + kTileN) * kLdsRow * 2; }
 
 hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
-    // K-quant rows are whole 256-value super-blocks; Q8_0 rows may end inside a slice
-    if (g.m <= 0 || g.k <= 0 || g.k % 32 || (g.w.type != 8 && g.k % kTileK) || g.w.k != (uint32_t)g.k ||
-        g.w.rows == 0)
-        return hipErrorInvalidValue;
-    const dim3 grid((g.w.rows + kTileN - 1) / kTileN, (g.m + kTileM - 1) / kTileM);
+    if (g.m <= 0 || g.k <= 0 || g.k % 32 || g.nseg < 1 || g.nseg > 3) return hipErrorInvalidValue;
+    int tiles = 0;
+    for (int i = 0; i < g.nseg; i++) {
+        const QMat& w = g.seg[i].w;
+        // K-quant rows are whole 256-value super-blocks; Q8_0 rows may end inside a tile
+        if (w.k != (uint32_t)g.k || w.rows == 0 || (w.type != 8 && g.k % 256) || g.seg[i].tile0 != tiles)
+            return hipErrorInvalidValue;
+        if (i < 2 && w.type != g.seg[0].w.type) return hipErrorInvalidValue;
+        tiles += (int)((w.rows + kTileN - 1) / kTileN);
+    }
+    const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
+    const dim3 grid(tiles, (g.m + kTileM - 1) / kTileM);
     const size_t lds = prefill_gemm_lds_bytes();
-#define RIBN_PG(T)                                                                                              \
-    {                                                                                                           \
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<T>),              \
+#define RIBN_PG(A, B)                                                                                           \
+    if (ta == A && tb == B) {                                                                                   \
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B>),           \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);               \
         if (e != hipSuccess) return e;                                                                          \
-        prefill_gemm_kernel<T><<<grid, kGemmThreads, lds, st>>>(g);                                             \
+        prefill_gemm_kernel<A, B><<<grid, kGemmThreads, lds, st>>>(g);                                          \
         return hipGetLastError();                                                                               \
     }
-    if (g.w.type == 12) RIBN_PG(12)
-    if (g.w.type == 14) RIBN_PG(14)
-    if (g.w.type == 8) RIBN_PG(8)
+    RIBN_PG(12, 12) RIBN_PG(14, 14) RIBN_PG(8, 8) RIBN_PG(12, 14) RIBN_PG(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
+    RIBN_PG(14, 8) RIBN_PG(8, 14)
 #undef RIBN_PG
     return hipErrorInvalidValue;
 }
