@@ -180,6 +180,11 @@ struct PrefillGemm {
     int mode;            // MV_STORE or MV_ADD
     int nseg;
     PrefillSeg seg[3];
+    // split-K: ksplit > 1 splits the K tiles over blockIdx.z; split z writes its
+    // partial sums (split 0 with the bias) to part + z m ldy, and a fixed-order
+    // reduction then writes y = (res) + sum of the partials
+    int ksplit;
+    float* part;
 };
 
 // Rows of one prefill chunk at positions pos0 .. pos0 + m - 1.
@@ -200,6 +205,8 @@ struct PrefillRows {
 };
 
 size_t prefill_gemm_lds_bytes();
+// split count launch_prefill_gemm would use for this GEMM (partials need ksplit * m * ldy floats)
+int prefill_gemm_splits(int m, int k, int n_tiles);
 hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t stream);
 hipError_t launch_rows_rms_f16(const float* x, int m, int k, const float* w, float eps, bool norm, uint16_t* out,
                                int ldo, hipStream_t stream);

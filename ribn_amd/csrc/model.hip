@@ -105,7 +105,8 @@ struct ribn_rocm_model {
 
     // chunked prefill buffers (prefill.hip), rows per chunk = chunk
     int chunk = 0;
-    float *p_h = nullptr, *p_qkv = nullptr, *p_q = nullptr, *p_gu = nullptr;
+    float *p_h = nullptr, *p_qkv = nullptr, *p_q = nullptr, *p_gu = nullptr, *p_part = nullptr;
+    size_t p_part_floats = 0;
     uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
 
     // persistent step (one launch per token); step_wg == 0: launch chain only
@@ -626,6 +627,9 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
             tiles += (int)((sg.w.rows + 127) / 128);
             g.nseg++;
         }
+        g.ksplit = prefill_gemm_splits(m, k, tiles);
+        if (g.ksplit > 1 && (size_t)g.ksplit * m * ldy <= M->p_part_floats) g.part = M->p_part;
+        else g.ksplit = 1;
         return launch_prefill_gemm(g, st);
     };
     for (int l = 0; l < M->L; l++) {
@@ -939,6 +943,14 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         HIPCHK(dalloc(M, &M->p_x16, 2 * c * kmax));
         HIPCHK(dalloc(M, &M->p_att16, 2 * c * qd));
         HIPCHK(dalloc(M, &M->p_act16, 2 * c * M->F));
+        // split-K partials: the largest split x ldy over the chunk's GEMMs
+        const int ldq = qd + 2 * kd;
+        auto need = [&](int k, int ldy, int tiles) { return (size_t)prefill_gemm_splits(M->chunk, k, tiles) * ldy; };
+        const int t_qkv = (qd + 127) / 128 + 2 * ((kd + 127) / 128), t_h = (M->H + 127) / 128, t_gu = 2 * ((M->F + 127) / 128);
+        size_t per_row = std::max(std::max(need(M->H, ldq, t_qkv), need(qd, M->H, t_h)),
+                                  std::max(need(M->H, 2 * M->F, t_gu), need(M->F, M->H, t_h)));
+        M->p_part_floats = per_row * c;
+        HIPCHK(dalloc(M, &M->p_part, sizeof(float) * M->p_part_floats));
     }
 
     const int slots = (int)M->max_seqs + 1;

@@ -182,10 +182,12 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
         acc[i][0] = f4_t{0.f, 0.f, 0.f, 0.f};
         acc[i][1] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
-    const int n_k = (g.k + kTileK - 1) / kTileK;
+    const int n_kt = (g.k + kTileK - 1) / kTileK;
+    const int ks = max(1, g.ksplit), z = blockIdx.z;
+    const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
     const int wr = tid >> 1, wq = tid & 1;   // dequant: row of the tile, quarter of the K tile
     const size_t wrow = (size_t)min(n0 + wr, n_rows - 1);
-    for (int kt = 0; kt < n_k; kt++) {
+    for (int kt = kt0; kt < kt1; kt++) {
         __syncthreads();
         // X slice: 128 rows x 128 halves = 2048 16-byte chunks, 8 per thread
 #pragma unroll
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     for (int nb = 0; nb < 2; nb++) {
         const int n = n0 + 32 * wave + 16 * nb + (lane & 15);
         if (n >= n_rows) continue;
-        const float bias = sg.bias ? sg.bias[n] : 0.f;
+        const float bias = sg.bias && z == 0 ? sg.bias[n] : 0.f;
 #pragma unroll
         for (int mb = 0; mb < 8; mb++) {
 #pragma unroll
@@ -229,11 +231,22 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
                 if (m >= g.m) continue;
                 const float v = (i == 0 ? acc[mb][nb].x : i == 1 ? acc[mb][nb].y : i == 2 ? acc[mb][nb].z : acc[mb][nb].w) + bias;
                 const size_t o = (size_t)m * g.ldy + sg.col0 + n;
-                if (g.mode == MV_ADD) g.y[o] = g.res[o] + v;
+                if (ks > 1) g.part[(size_t)z * g.m * g.ldy + o] = v;
+                else if (g.mode == MV_ADD) g.y[o] = g.res[o] + v;
                 else g.y[o] = v;
             }
         }
     }
+}
+
+// y = (res) + sum over z of part[z] (fixed order: deterministic)
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int ks, size_t n, const float* res,
+                                                            float* y, int add) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = add ? res[i] : 0.f;
+    for (int z = 0; z < ks; z++) v += part[(size_t)z * n + i];
+    y[i] = v;
 }
 
 // rows x[m][k] -> f16(rms_norm(x) * w) (rms_norm, model_ops.rs:108-157); w may be null
@@ -476,6 +489,15 @@ hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
 
 }  // namespace
 
+int prefill_gemm_splits(int m, int k, int n_tiles) {
+    // enough workgroups for two per CU on 256 CUs, at least 4 K tiles per split, at most 8 splits
+    const int wgs = n_tiles * ((m + kTileM - 1) / kTileM);
+    const int n_kt = (k + kTileK - 1) / kTileK;
+    int ks = 1;
+    while (ks < 8 && wgs * ks < 512 && n_kt / (2 * ks) >= 4) ks *= 2;
+    return ks;
+}
+
 size_t prefill_gemm_lds_bytes() { return (size_t)(kTileM + kTileN) * kLdsRow * 2; }
 
 hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
@@ -490,14 +512,23 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
         tiles += (int)((w.rows + kTileN - 1) / kTileN);
     }
     const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
-    const dim3 grid(tiles, (g.m + kTileM - 1) / kTileM);
+    const int ks = g.part ? max(1, g.ksplit) : 1;
+    if (ks > 1 && ks > (g.k + kTileK - 1) / kTileK) return hipErrorInvalidValue;
+    const dim3 grid(tiles, (g.m + kTileM - 1) / kTileM, ks);
+    PrefillGemm gg = g;
+    gg.ksplit = ks;
     const size_t lds = prefill_gemm_lds_bytes();
 #define RIBN_PG(A, B)                                                                                           \
     if (ta == A && tb == B) {                                                                                   \
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B>),           \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);               \
         if (e != hipSuccess) return e;                                                                          \
-        prefill_gemm_kernel<A, B><<<grid, kGemmThreads, lds, st>>>(g);                                          \
+        prefill_gemm_kernel<A, B><<<grid, kGemmThreads, lds, st>>>(gg);                                         \
+        e = hipGetLastError();                                                                                  \
+        if (e != hipSuccess || ks == 1) return e;                                                               \
+        const size_t n = (size_t)g.m * g.ldy;                                                                   \
+        splitk_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g.part, ks, n, g.res, g.y,            \
+                                                                          g.mode == MV_ADD ? 1 : 0);            \
         return hipGetLastError();                                                                               \
     }
     RIBN_PG(12, 12) RIBN_PG(14, 14) RIBN_PG(8, 8) RIBN_PG(12, 14) RIBN_PG(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
