@@ -180,7 +180,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k/q6_k weights x int8 (two-level) staged activations, int32/fp32 accumulate, f16 KV",
+        "dtype": "decode: q4_k/q6_k weights x 16-bit fixed-point activations (int32 dot, fp32 combine); prefill: f16 MFMA operands, fp32 accumulate; f16 KV",
         "data": "synthetic (seeded N(0,0.02) weights quantized to GGUF Q4_K_M; random prompt)",
         "config": {"workload": "qwen3-8b-shape Q4_K_M bs1 greedy decode (BASELINE configs[2])",
                    "prompt": args.prompt, "decode_tokens": args.steps, "layers": info.layers,

@@ -27,16 +27,54 @@ __device__ __forceinline__ uint32_t dword_at(const u4_t& v, uint32_t i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Cross-lane reductions without LDS traffic: DPP within rows of 16 lanes
+// (quad permutes, then half-row and row mirrors, each of which pairs lanes that
+// already hold equal partial results) and the gfx950 permlane swaps across rows.
+// They need every lane of the wave active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// v + (v of lane ^ 16), v + (v of lane ^ 32): the swap returns the pair {own, partner}
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// sum / maximum over aligned groups of W lanes (W = 4, 8, 16, 32 or 64), result in every lane
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) v += dpp_f<0x141>(v);   // row_half_mirror
+    if constexpr (W >= 16) v += dpp_f<0x140>(v);  // row_mirror
+    if constexpr (W >= 32) v = xor16_sum(v);
+    if constexpr (W >= 64) v = xor32_sum(v);
     return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+    if constexpr (W >= 32) v = xor16_max(v);
+    if constexpr (W >= 64) v = xor32_max(v);
     return v;
 }
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
@@ -590,6 +628,7 @@ __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWor
 struct NoSync {
     __device__ __forceinline__ bool operator()() const { return true; }
     __device__ __forceinline__ void mark() const {}
+    __device__ __forceinline__ void phase(int) const {}   // profiling hook inside attention_item
 };
 
 // One workgroup's share of a matvec launch laid out in `a` (segments, items per
@@ -707,10 +746,11 @@ template <int HD, int G>
 struct AttnLds {
     static constexpr int NS = kThreads / (HD / 8);
     float buf[G + 2][HD];                // q heads, k, v of the current token
+    float rp[HD];                        // rope cos | sin
     uint16_t kt[kTile][HD];
     uint16_t vt[kTile][HD];
     float sc[G][kMaxSplitTokens];        // scores, then probabilities
-    float red[NS][HD];                   // P.V reduction
+    float red[kWaves][G * HD];           // P.V: one partial per wave
     float stat[2][G];                    // per-head max, sum
     int pg[kMaxSplitTokens / kPageTokens];
 };
@@ -738,21 +778,49 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     auto& pg = L.pg;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int qd = a.hq * HD, kd = a.hkv * HD;
-    constexpr int NRAW = (G + 2 + (kThreads / HD) - 1) / (kThreads / HD);
-    float rawv[NRAW];   // q/k/v rows of this KV head
+    // prologue layout: LPR lanes per row, 4 consecutive values per lane
+    constexpr int LPR = HD / 4;
+    constexpr int RPP = kThreads / LPR;              // rows per pass
+    constexpr int NP = (G + 2 + RPP - 1) / RPP;      // passes over q heads, k, v
+    const int pc = tid % LPR, pr = tid / LPR;
+    float4 rawv[NP];
     auto load_rawv = [&]() {
 #pragma unroll
-        for (int j = 0; j < NRAW; j++) {
-            const int i = j * kThreads + tid;
-            if (i < (G + 2) * HD) {
-                const int r = i / HD, d = i % HD;
+        for (int j = 0; j < NP; j++) {
+            const int r = j * RPP + pr;
+            rawv[j] = float4{0.f, 0.f, 0.f, 0.f};
+            if (r < G + 2) {
                 const float* src = r < G ? a.raw + (size_t)(kvh * G + r) * HD
                                          : (r == G ? a.raw + qd + kvh * HD : a.raw + qd + kd + kvh * HD);
-                rawv[j] = src[d];
+                rawv[j] = *reinterpret_cast<const float4*>(src + 4 * pc);
             }
         }
     };
-    if constexpr (!PERSIST) load_rawv();
+    // head-norm weights and rope cos/sin for this lane's columns, fetched with
+    // q/k/v so the prologue makes no global load of its own. With rot == HD the
+    // rotation pairs column c with c +- HD/2, which sits LPR/2 lanes away.
+    const int half = a.rot / 2;
+    const bool rope_regs = a.rot == HD;
+    float4 nwq{0.f, 0.f, 0.f, 0.f}, nwk{0.f, 0.f, 0.f, 0.f};
+    if (a.q_norm) {
+        nwq = *reinterpret_cast<const float4*>(a.q_norm + 4 * pc);
+        nwk = *reinterpret_cast<const float4*>(a.k_norm + 4 * pc);
+    }
+    float4 rc{1.f, 1.f, 1.f, 1.f}, rs{0.f, 0.f, 0.f, 0.f};
+    float rpv = 0.f;
+    auto load_rope = [&]() {
+        if (rope_regs) {
+            const int p0 = (4 * pc) % half;
+            rc = *reinterpret_cast<const float4*>(a.rope + p0);
+            rs = *reinterpret_cast<const float4*>(a.rope + half + p0);
+        } else if (tid < a.rot) {
+            rpv = a.rope[tid];
+        }
+    };
+    if constexpr (!PERSIST) {
+        load_rawv();
+        load_rope();
+    }
     const int ctx = pos + 1;
     int per = (ctx + a.n_splits - 1) / a.n_splits;
     per = (per + kPageTokens - 1) / kPageTokens * kPageTokens;
@@ -766,6 +834,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     const int t0 = split * per, t1 = min(ctx, t0 + per), n = max(0, t1 - t0);
     const bool owner = t0 <= pos && pos < t1;
 
+    sync.phase(0);
     __syncthreads();   // LDS may still be in use by this workgroup's previous work item
     for (int i = tid; i < n; i += kThreads)
         if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = pages[(t0 + i) / kPageTokens];
@@ -773,50 +842,91 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     KvTile<HD, F16> kpre, vpre;   // first tile in flight during the prologue
     kpre.load(a.kcache, pg, a.hkv, kvh, 0, n, t0);
     vpre.load(a.vcache, pg, a.hkv, kvh, 0, n, t0);
+    sync.phase(1);
     if (!sync()) return false;
-    if constexpr (PERSIST) load_rawv();
-#pragma unroll
-    for (int j = 0; j < NRAW; j++) {
-        const int i = j * kThreads + tid;
-        if (i < (G + 2) * HD) buf[i / HD][i % HD] = rawv[j];
+    if constexpr (PERSIST) {
+        load_rawv();
+        load_rope();
     }
-    __syncthreads();
+    if (!rope_regs && tid < a.rot) L.rp[tid] = rpv;
 
-    // -- prologue: per-head norm, rope, current token at cache precision
-    if (a.q_norm) {
-        for (int r = wave; r <= G; r += kWaves) {
-            const float* nw = r < G ? a.q_norm : a.k_norm;
-            float ss = 0.f;
-            for (int d = lane; d < HD; d += 64) ss += buf[r][d] * buf[r][d];
-            ss = wave_sum(ss);
+    sync.phase(2);
+    // -- prologue in registers: per-head norm, rope, q scaled into the log2
+    //    domain, the current token's k and v at cache precision
+    uint2 cur_k{0u, 0u}, cur_v{0u, 0u};
+    bool hold_k = false, hold_v = false;
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        const int r = j * RPP + pr;
+        float v[4] = {rawv[j].x, rawv[j].y, rawv[j].z, rawv[j].w};
+        if (a.q_norm) {
+            float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+            ss = group_sum<LPR>(ss);
             const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
-            for (int d = lane; d < HD; d += 64) buf[r][d] = buf[r][d] * inv * nw[d];
+            const float4 nw = r < G ? nwq : nwk;
+            if (r <= G) {
+                v[0] = v[0] * inv * nw.x; v[1] = v[1] * inv * nw.y;
+                v[2] = v[2] * inv * nw.z; v[3] = v[3] * inv * nw.w;
+            }
+        }
+        if (rope_regs) {
+            float o4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o4[i] = __shfl_xor(v[i], LPR / 2);
+            if (r <= G) {
+                const float c[4] = {rc.x, rc.y, rc.z, rc.w}, sn[4] = {rs.x, rs.y, rs.z, rs.w};
+                const bool first = 4 * pc < half;
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = first ? v[i] * c[i] - o4[i] * sn[i] : o4[i] * sn[i] + v[i] * c[i];
+            }
+        }
+        if (r < G + 1 && !rope_regs) {
+            *reinterpret_cast<float4*>(&buf[r][4 * pc]) = float4{v[0], v[1], v[2], v[3]};
+        } else if (r < G) {
+            *reinterpret_cast<float4*>(&buf[r][4 * pc]) =
+                float4{v[0] * a.scale_log2, v[1] * a.scale_log2, v[2] * a.scale_log2, v[3] * a.scale_log2};
+        } else if (r == G) {
+            cur_k = uint2{kv_encode(v[0], F16 ? 1 : 0) | (uint32_t)kv_encode(v[1], F16 ? 1 : 0) << 16,
+                          kv_encode(v[2], F16 ? 1 : 0) | (uint32_t)kv_encode(v[3], F16 ? 1 : 0) << 16};
+            hold_k = true;
+        }
+        if (r == G + 1) {
+            cur_v = uint2{kv_encode(v[0], F16 ? 1 : 0) | (uint32_t)kv_encode(v[1], F16 ? 1 : 0) << 16,
+                          kv_encode(v[2], F16 ? 1 : 0) | (uint32_t)kv_encode(v[3], F16 ? 1 : 0) << 16};
+            hold_v = true;
+        }
+    }
+    if (!rope_regs) {
+        // partial rotary: rotate the first rot columns through LDS
+        __syncthreads();
+        for (int i = tid; i < (G + 1) * half; i += kThreads) {
+            const int r = i / half, p = i % half;
+            const float c = L.rp[p], sn = L.rp[half + p];
+            const float x0 = buf[r][p], x1 = buf[r][p + half];
+            buf[r][p] = x0 * c - x1 * sn;
+            buf[r][p + half] = x0 * sn + x1 * c;
         }
         __syncthreads();
-    }
-    const int half = a.rot / 2;
-    for (int i = tid; i < (G + 1) * half; i += kThreads) {
-        const int r = i / half, p = i % half;
-        const float c = a.rope[p], sn = a.rope[half + p];
-        const float x0 = buf[r][p], x1 = buf[r][p + half];
-        buf[r][p] = x0 * c - x1 * sn;
-        buf[r][p + half] = x0 * sn + x1 * c;
-    }
-    __syncthreads();
-    uint16_t cur_e = 0;
-    if (tid < 2 * HD) {
-        const int r = G + tid / HD, d = tid % HD;
-        cur_e = kv_encode(buf[r][d], F16 ? 1 : 0);
-        if (owner) {
-            const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
-            uint16_t* dst = (r == G ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
-            dst[d] = cur_e;
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int r = j * RPP + pr;
+            if (r == G) {
+                const float4 k4 = *reinterpret_cast<const float4*>(&buf[G][4 * pc]);
+                cur_k = uint2{kv_encode(k4.x, F16 ? 1 : 0) | (uint32_t)kv_encode(k4.y, F16 ? 1 : 0) << 16,
+                              kv_encode(k4.z, F16 ? 1 : 0) | (uint32_t)kv_encode(k4.w, F16 ? 1 : 0) << 16};
+                hold_k = true;
+            }
         }
+        for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
     }
-    // scale q into the log2 domain
-    for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
+    if (owner && (hold_k || hold_v)) {
+        const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
+        uint16_t* dst = (hold_k ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
+        *reinterpret_cast<uint2*>(dst + 4 * pc) = hold_k ? cur_k : cur_v;
+    }
     __syncthreads();
 
+    sync.phase(3);
     // -- scores, tile by tile: lane group of 4 per position
     const int stl = tid >> 2, part = tid & 3;
     for (int c0 = 0; c0 < n; c0 += kTile) {
@@ -828,7 +938,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         }
         if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
             __syncthreads();
-            if (tid < HD) kt[pos - t0 - c0][tid] = cur_e;
+            if (hold_k) *reinterpret_cast<uint2*>(&kt[pos - t0 - c0][4 * pc]) = cur_k;
         }
         __syncthreads();
         const int tl = c0 + stl;
@@ -853,8 +963,8 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            acc[g] += __shfl_xor(acc[g], 1);
-            acc[g] += __shfl_xor(acc[g], 2);
+            acc[g] += dpp_f<0xB1>(acc[g]);
+            acc[g] += dpp_f<0x4E>(acc[g]);
         }
         if (part == 0 && tl < n) {
 #pragma unroll
@@ -863,6 +973,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         __syncthreads();
     }
 
+    sync.phase(4);
     // -- softmax statistics per head
     for (int g = wave; g < G; g += kWaves) {
         float m = -INFINITY;
@@ -879,6 +990,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     }
     __syncthreads();
 
+    sync.phase(5);
     // -- o[g] = sum_t p[g][t] v[t]
     const int ch = tid % CH, sl = tid / CH;
     float o[G][8];
@@ -896,7 +1008,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         }
         if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
             __syncthreads();
-            if (tid >= HD && tid < 2 * HD) vt[pos - t0 - c0][tid - HD] = cur_e;
+            if (hold_v) *reinterpret_cast<uint2*>(&vt[pos - t0 - c0][4 * pc]) = cur_v;
         }
         __syncthreads();
         const int lim = min(kTile, n - c0);
@@ -917,69 +1029,116 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
             }
         }
     }
+    sync.phase(6);
     const bool direct = a.n_splits == 1;
     float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
+    // the slices of one wave (lanes CH apart) reduce in registers, the waves in LDS
 #pragma unroll
-    for (int g = 0; g < G; g++) {
+    for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) red[sl][ch * 8 + i] = o[g][i];
-        __syncthreads();
-        if (tid < HD) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < NS; j++) acc += red[j][tid];
-            if (direct) st_agent(a.out + (size_t)(kvh * G + g) * HD + tid, acc / stat[1][g]);
-            else st_agent(rec + g * HD + tid, acc);
+        for (int i = 0; i < 8; i++) {
+            float t = o[g][i];
+            if constexpr (CH == 8) t += dpp_f<0x128>(t);   // row_ror:8 = lane ^ 8 within a row
+            t = xor16_sum(t);
+            o[g][i] = xor32_sum(t);
         }
-        __syncthreads();
+    if (lane < CH) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i += 4)
+                *reinterpret_cast<float4*>(&red[wave][g * HD + ch * 8 + i]) =
+                    float4{o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]};
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) acc += red[w][idx];
+        if (direct) st_agent(a.out + (size_t)kvh * G * HD + idx, acc / stat[1][idx / HD]);
+        else st_agent(rec + idx, acc);
     }
     if (direct) return true;
     if (tid < G) {
         st_agent(rec + G * HD + tid, n > 0 ? stat[0][tid] : -INFINITY);
         st_agent(rec + G * HD + G + tid, n > 0 ? stat[1][tid] : 0.f);
     }
+    sync.phase(7);
     if (!arrive_last(a.counters + kvh, a.n_splits)) return true;
+    sync.phase(8);
 
     // -- merge the splits of this KV head (log-sum-exp in base 2). The split
-    //    statistics are fetched in one parallel batch, then each output
-    //    element's partials with all loads issued before any is used.
+    //    statistics and the first batch of every output element's partials are
+    //    all in flight at once: one round trip for up to SB splits.
+    constexpr int NE = (G * HD + kThreads - 1) / kThreads;   // output elements per thread
+    constexpr int SB = NE <= 2 ? 16 : 8;                      // splits per batch
+    constexpr int GPW = (G + kWaves - 1) / kWaves;   // heads per wave in the statistics
+    constexpr int SPL = kMaxSplits / 64;               // splits per lane
     const float* base = a.part + (size_t)kvh * a.n_splits * REC;
-    float* smx = &sc[0][0];                        // [G][n_splits] maxima (scores are dead)
-    float* swt = &sc[0][0] + G * kMaxSplits;       // [G][n_splits] weights
-    for (int i = tid; i < G * a.n_splits; i += kThreads) {
-        const int g = i / a.n_splits, sp = i % a.n_splits;
-        smx[i] = ld_agent(base + (size_t)sp * REC + G * HD + g);
-        swt[i] = ld_agent(base + (size_t)sp * REC + G * HD + G + g);
+    float* swt = &sc[0][0];                            // [G][n_splits] weights (scores are dead)
+    float mv[GPW][SPL], lv[GPW][SPL];
+#pragma unroll
+    for (int gi = 0; gi < GPW; gi++)
+#pragma unroll
+        for (int si = 0; si < SPL; si++) {
+            const int g = wave + gi * kWaves, sp = lane + si * 64;
+            const bool ok = g < G && sp < a.n_splits;
+            mv[gi][si] = ok ? ld_agent(base + (size_t)sp * REC + G * HD + g) : -INFINITY;
+            lv[gi][si] = ok ? ld_agent(base + (size_t)sp * REC + G * HD + G + g) : 0.f;
+        }
+    float pv[NE][SB];
+    auto load_batch = [&](int sp0) {
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const int idx = e * kThreads + tid;
+#pragma unroll
+            for (int j = 0; j < SB; j++)
+                pv[e][j] = idx < G * HD && sp0 + j < a.n_splits ? ld_agent(base + (size_t)(sp0 + j) * REC + idx) : 0.f;
+        }
+    };
+    load_batch(0);
+    // one wave per head: lanes hold the splits
+#pragma unroll
+    for (int gi = 0; gi < GPW; gi++) {
+        const int g = wave + gi * kWaves;
+        if (g < G) {   // wave-uniform
+            float mx = -INFINITY;
+#pragma unroll
+            for (int si = 0; si < SPL; si++) mx = fmaxf(mx, mv[gi][si]);
+            mx = wave_max(mx);
+            float lt = 0.f;
+#pragma unroll
+            for (int si = 0; si < SPL; si++) {
+                const int sp = lane + si * 64;
+                const float wgt = mv[gi][si] == -INFINITY ? 0.f : exp2f(mv[gi][si] - mx);
+                lt += lv[gi][si] * wgt;
+                if (sp < a.n_splits) swt[g * a.n_splits + sp] = wgt;
+            }
+            lt = wave_sum(lt);
+            if (lane == 0) stat[1][g] = lt;
+        }
     }
     __syncthreads();
-    if (tid < G) {
-        float mx = -INFINITY;
-        for (int sp = 0; sp < a.n_splits; sp++) mx = fmaxf(mx, smx[tid * a.n_splits + sp]);
-        float lt = 0.f;
-        for (int sp = 0; sp < a.n_splits; sp++) {
-            const float ms = smx[tid * a.n_splits + sp];
-            const float wgt = ms == -INFINITY ? 0.f : exp2f(ms - mx);
-            lt += swt[tid * a.n_splits + sp] * wgt;
-            swt[tid * a.n_splits + sp] = wgt;
-        }
-        stat[1][tid] = lt;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD;
-        const float* w8 = swt + g * a.n_splits;
-        float acc = 0.f;
-        for (int sp0 = 0; sp0 < a.n_splits; sp0 += 8) {
-            float v[8];
+    float acc[NE];
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                v[j] = sp0 + j < a.n_splits ? ld_agent(base + (size_t)(sp0 + j) * REC + idx) : 0.f;
+    for (int e = 0; e < NE; e++) acc[e] = 0.f;
+    for (int sp0 = 0; sp0 < a.n_splits; sp0 += SB) {
+        if (sp0 > 0) load_batch(sp0);
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (sp0 + j < a.n_splits) acc = fmaf(v[j], w8[sp0 + j], acc);
+        for (int e = 0; e < NE; e++) {
+            const int idx = e * kThreads + tid;
+            const float* w8 = swt + (idx < G * HD ? idx / HD : 0) * a.n_splits;
+#pragma unroll
+            for (int j = 0; j < SB; j++)
+                if (sp0 + j < a.n_splits) acc[e] = fmaf(pv[e][j], w8[sp0 + j], acc[e]);
         }
-        st_agent(a.out + (size_t)kvh * G * HD + idx, acc / stat[1][g]);
     }
+#pragma unroll
+    for (int e = 0; e < NE; e++) {
+        const int idx = e * kThreads + tid;
+        if (idx < G * HD) st_agent(a.out + (size_t)kvh * G * HD + idx, acc[e] / stat[1][idx / HD]);
+    }
+    sync.phase(9);
     return true;
 }
 

@@ -1672,6 +1672,8 @@ extern "C" int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t* blocks, uint
     g.x = dx16; g.m = (int)m; g.k = (int)k; g.y = dy; g.ldy = (int)rows; g.mode = MV_STORE;
     g.nseg = 1;
     g.seg[0].w = q;
+    g.ksplit = prefill_gemm_splits((int)m, (int)k, (int)((rows + 127) / 128));
+    if (g.ksplit > 1) HIPCHK(S.alloc(&g.part, sizeof(float) * g.ksplit * m * rows));
     HIPCHK(launch_prefill_gemm(g, nullptr));
     HIPCHK(hipMemcpy(y, dy, sizeof(float) * m * rows, hipMemcpyDeviceToHost));
     return RIBN_OK;

@@ -78,6 +78,7 @@ struct GridSync {
     __device__ __forceinline__ void mark() const {
         if (stamp && threadIdx.x == 0) stamp[(*ns)++] = wall_clock64();
     }
+    __device__ __forceinline__ void phase(int) const {}
     __device__ __forceinline__ bool operator()() const {
         mark();
         const bool ok = grid_sync(bar, n, deadline);
@@ -90,6 +91,7 @@ struct GridSync {
 struct OnceSync {
     const GridSync& g;
     bool done;
+    __device__ __forceinline__ void phase(int) const {}
     __device__ __forceinline__ bool operator()() {
         if (done) return true;
         done = true;
