@@ -70,6 +70,7 @@ __device__ __forceinline__ bool grid_sync(uint32_t* bar, uint32_t n, uint64_t de
 }
 
 struct GridSync {
+    static constexpr bool kEarlyX = false;   // the input is written by the previous stage
     uint32_t* bar;
     uint32_t n;
     uint64_t deadline;
@@ -91,6 +92,7 @@ struct GridSync {
 struct OnceSync {
     const GridSync& g;
     bool done;
+    static constexpr bool kEarlyX = false;
     __device__ __forceinline__ void phase(int) const {}
     __device__ __forceinline__ bool operator()() {
         if (done) return true;
