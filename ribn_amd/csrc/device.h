@@ -214,91 +214,129 @@ __device__ __forceinline__ void plane_of_group(int g, int& unit, int& plane, int
     }
 }
 
-// The first staging pass's input (x and the norm weights of groups 0..255),
-// loaded before the weight stream of a standalone launch so it returns ahead of
-// the weights (loads complete in order).
+// The input of the first NP staging passes (x of groups 0..256 NP - 1, and the
+// norm weights of the first pass), loaded before the weight stream of a
+// standalone launch so it returns ahead of the weights (loads complete in order).
+template <int NP>
 struct XPre {
-    float4 x[4];
+    float4 x[NP][4];
     float4 w[4];
 };
-__device__ __forceinline__ void stage_pre(const float* x, const float* norm_w, int k, XPre& p) {
-    const int g = threadIdx.x;
+template <int NP>
+__device__ __forceinline__ void stage_pre(const float* x, const float* norm_w, int k, XPre<NP>& p) {
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int g = q * kThreads + threadIdx.x;
+        const bool valid = g < k / 16;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            p.x[q][j] = valid ? reinterpret_cast<const float4*>(x)[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bool valid = (int)threadIdx.x < k / 16;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        p.w[j] = valid && norm_w ? reinterpret_cast<const float4*>(norm_w)[threadIdx.x * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
+}
+
+// One thread's group g of 16 inputs: x (times the norm weights, when given)
+// quantized to 16-bit fixed point into the unit planes, the block scale and the
+// group sum into gs; ss gathers the sum of squares of x. All lanes take part
+// (the block maximum is a quad reduction).
+template <int T>
+__device__ __forceinline__ void stage_group(int g, int k, const float4 (&xv)[4], const float4* wv, int8_t* xs,
+                                            float* gs, float& ss) {
+    const int n_units = T == 8 ? k / 16 : k / 32;
     const bool valid = g < k / 16;
+    u4_t* planes = reinterpret_cast<u4_t*>(xs);
+    float v[16];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        p.x[j] = valid ? reinterpret_cast<const float4*>(x)[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
-        p.w[j] = valid && norm_w ? reinterpret_cast<const float4*>(norm_w)[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
+        float4 t = valid ? xv[j] : float4{0.f, 0.f, 0.f, 0.f};
+        ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
+        if (wv && valid) {
+            const float4 w = wv[j];
+            t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
+        }
+        v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+    }
+    float am = 0.f, sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        am = fmaxf(am, fabsf(v[j]));
+        sum += v[j];
+    }
+    // maximum over the 4 lanes of a quad (the four groups of a 64-value block)
+    am = fmaxf(am, dpp_f<0xB1>(am));
+    am = fmaxf(am, dpp_f<0x4E>(am));
+    // x ~ s * v16 with v16 = rint(x / s) in [-32512, 32512], s = max|x| / 32512
+    // over the 64-value block; v16 = 256 hi + lo with hi, lo signed bytes
+    const float sc = am * (1.0f / 32512.0f);
+    const float is = am > 0.f ? 32512.0f / am : 0.f;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t h4 = 0, l4 = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int q = (int)rintf(v[4 * j + b] * is);
+            const int hi = (q + 128) >> 8, lo = q - (hi << 8);
+            h4 |= ((uint32_t)hi & 0xffu) << (8 * b);
+            l4 |= ((uint32_t)lo & 0xffu) << (8 * b);
+        }
+        hw[j] = h4;
+        lw[j] = l4;
+    }
+    if (valid) {
+        int unit, plane, slot;
+        plane_of_group<T>(g, unit, plane, slot);
+        planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
+        planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
+        if constexpr (T == 8) {
+            gs[unit * 2] = sc;
+            gs[unit * 2 + 1] = sum;
+        } else {
+            gs[unit * 4 + slot] = sc;
+            gs[unit * 4 + 2 + slot] = sum;
+        }
     }
 }
 
-template <int T, bool PRE = false>
+// Stage x (k values, RMSNorm weights optional) into LDS for the matvec; returns
+// the RMSNorm inverse 1/sqrt(mean x^2 + eps) (1 without norm), which the
+// epilogue applies to the row sums. The first NP passes take their input from
+// `pre` (loaded by stage_pre).
+template <int T, int NP = 0>
 __device__ float stage_x(const float* x, const float* norm_w, float eps, int k, int8_t* xs, float* gs, float* red,
-                         const XPre* pre = nullptr) {
+                         const XPre<NP == 0 ? 1 : NP>* pre = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4* x4 = reinterpret_cast<const float4*>(x);
     const float4* w4 = reinterpret_cast<const float4*>(norm_w);
     const bool norm = norm_w != nullptr;
-    const int n_units = T == 8 ? k / 16 : k / 32;
     const int n16 = k / 16;
-    u4_t* planes = reinterpret_cast<u4_t*>(xs);
     float ss = 0.f;
     // thread = one group of 16 values; the four groups of a 64-value block sit in
     // four consecutive lanes, which share the block's scale
-    for (int base = 0; base < n16; base += kThreads) {
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int g = q * kThreads + tid;
+        if (q * kThreads < n16) {   // uniform
+            float4 wl[4];
+            if (norm && q > 0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) wl[j] = g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
+            }
+            stage_group<T>(g, k, pre->x[q], norm ? (q == 0 ? pre->w : wl) : nullptr, xs, gs, ss);
+        }
+    }
+    for (int base = NP * kThreads; base < n16; base += kThreads) {
         const int g = base + tid;
-        const bool valid = g < n16;
-        float v[16];
+        float4 xl[4], wl[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const bool first = PRE && base == 0;
-            float4 t = first ? pre->x[j] : valid ? x4[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
-            ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-            if (norm && valid) {
-                const float4 w = first ? pre->w[j] : w4[g * 4 + j];
-                t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
-            }
-            v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+            xl[j] = g < n16 ? x4[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
+            if (norm) wl[j] = g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
         }
-        float am = 0.f, sum = 0.f;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            am = fmaxf(am, fabsf(v[j]));
-            sum += v[j];
-        }
-        // maximum over the 4 lanes of a quad: DPP quad permutes (lane ^ 1, lane ^ 2)
-        am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0xB1, 0xF, 0xF, true)));
-        am = fmaxf(am, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(am), 0x4E, 0xF, 0xF, true)));
-        // x ~ s * v16 with v16 = rint(x / s) in [-32512, 32512], s = max|x| / 32512
-        // over the 64-value block; v16 = 256 hi + lo with hi, lo signed bytes
-        const float sc = am * (1.0f / 32512.0f);
-        const float is = am > 0.f ? 32512.0f / am : 0.f;
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            uint32_t h4 = 0, l4 = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int q = (int)rintf(v[4 * j + b] * is);
-                const int hi = (q + 128) >> 8, lo = q - (hi << 8);
-                h4 |= ((uint32_t)hi & 0xffu) << (8 * b);
-                l4 |= ((uint32_t)lo & 0xffu) << (8 * b);
-            }
-            hw[j] = h4;
-            lw[j] = l4;
-        }
-        if (valid) {
-            int unit, plane, slot;
-            plane_of_group<T>(g, unit, plane, slot);
-            planes[plane * n_units + unit] = u4_t{hw[0], hw[1], hw[2], hw[3]};
-            planes[(plane + 1) * n_units + unit] = u4_t{lw[0], lw[1], lw[2], lw[3]};
-            if constexpr (T == 8) {
-                gs[unit * 2] = sc;
-                gs[unit * 2 + 1] = sum;
-            } else {
-                gs[unit * 4 + slot] = sc;
-                gs[unit * 4 + 2 + slot] = sum;
-            }
-        }
+        stage_group<T>(g, k, xl, norm ? wl : nullptr, xs, gs, ss);
     }
     float inv = 1.0f;
     if (norm) {
@@ -574,8 +612,10 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
                                         float* red, uint64_t& best, Sync&& sync) {
     const int total = w.n_items * w.ngr;
     constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX;
-    XPre pre;
-    if constexpr (EARLY) stage_pre(a.x, a.norm_w, a.k, pre);
+    // the residual launches (O, down) take a long input without norm: three passes early
+    constexpr int NP = EARLY ? (MODE == MV_ADD ? 3 : 1) : 0;
+    XPre<NP == 0 ? 1 : NP> pre;
+    if constexpr (NP > 0) stage_pre<NP>(a.x, a.norm_w, a.k, pre);
     const float addend = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE) : 0.f;
     Group<T> ring[D];
     Cursor ld{0, 0};
@@ -590,7 +630,7 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     const float* const norm_w = a.norm_w;
     const float eps = a.eps;
     const int k = a.k;
-    const float oscale = stage_x<T, EARLY>(x, norm_w, eps, k, xs, gs, red, &pre);
+    const float oscale = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);
     sync.mark();
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
     float a0 = 0.f, b0 = 0.f;
