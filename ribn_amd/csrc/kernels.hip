@@ -55,7 +55,20 @@ __global__ void advance_kernel(const StepCtl* ctl) {
     if (threadIdx.x == 0) ctl->seq->pos += 1;
 }
 
-constexpr int kRingStandalone = 3;
+// Ring depth (load groups in flight per wave) of the standalone matvec, per type.
+#ifndef RIBN_RING_SA_Q4
+#define RIBN_RING_SA_Q4 3
+#endif
+#ifndef RIBN_RING_SA_Q6
+#define RIBN_RING_SA_Q6 3
+#endif
+#ifndef RIBN_RING_SA_Q8
+#define RIBN_RING_SA_Q8 3
+#endif
+template <int T>
+constexpr int ring_standalone() {
+    return T == 12 ? RIBN_RING_SA_Q4 : T == 14 ? RIBN_RING_SA_Q6 : RIBN_RING_SA_Q8;
+}
 
 // Fused dequant-matvec (gguf_gemv qwen_reference.rs:31-40; q*_gemv_warp
 // kernels/quantized/q4_k.cu:103, q6_k.cu:45, q8_0.cu:27). Each wave computes
@@ -65,7 +78,7 @@ template <int TA, int TB, int MODE>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint64_t best = 0ull;
-    mv_wg<TA, TB, MODE, kRingStandalone, kRingStandalone>(a, blockIdx.x, lds, best, NoSync{});
+    mv_wg<TA, TB, MODE, ring_standalone<TA>(), ring_standalone<TB>()>(a, blockIdx.x, lds, best, NoSync{});
     if constexpr (MODE == MV_HEAD) head_finish(a, best, blockIdx.x, gridDim.x);
 }
 

@@ -13,6 +13,7 @@
 #include <hip/hip_fp16.h>
 
 #include "kernels.h"
+#include "lanes.h"
 
 namespace ribn {
 namespace {
@@ -373,91 +374,188 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(PrefillRows p) {
     }
 }
 
-__device__ __forceinline__ float kv_val(uint16_t b, int f16) {
-    return f16 ? __half2float(__ushort_as_half(b)) : __uint_as_float((uint32_t)b << 16);
-}
 
 // Causal attention of a chunk's rows over the paged cache (positions 0 .. own
-// position; attn_score_gqa_paged rows > 1, model_ops.rs:442-554). Workgroup =
-// 16 chunk rows x the G query heads of one KV head; TP threads per (row, head)
-// pair split head_dim; keys in tiles of 32 with an fp32 online softmax.
-constexpr int kAttRows = 16;
+// position; attn_score_gqa_paged rows > 1, model_ops.rs:442-554), flash style
+// on MFMA. Workgroup = RB blocks of 16 chunk rows x the G query heads of one
+// KV head; a (row block, head) tile belongs to one wave. Per 32-key tile:
+//   S^T[key][q] = K Q^T   (v_mfma_f32_16x16x32_f16, A = K rows from LDS,
+//                          B = q in registers, binary16 with log2(e)/sqrt(hd) folded in)
+//   online softmax per query in fp32 (exp2), P rounded to binary16
+//   O^T[dim][q] += V^T P^T (A = V^T from a transposed LDS tile, B = P^T taken
+//                          straight from the S^T accumulators)
+// The S^T / O^T orientation keeps every per-query quantity in lane % 16, so the
+// softmax needs no transposes: a lane's P^T entries are keys 4j..4j+3 and
+// 16+4j..16+4j+3 (j = lane / 16), and V^T is read in the same key order.
+// A binary16 cache is used as stored; a bfloat16 cache is converted to binary16
+// when staged (exact for values in binary16's normal range).
 constexpr int kAttKeys = 32;
 
-template <int HD, int G>
+template <int HD, int G, bool F16KV>
 __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
-    constexpr int PAIRS = kAttRows * G;
-    constexpr int TP0 = 256 / PAIRS;
-    constexpr int TP = TP0 >= 16 ? 16 : TP0 >= 8 ? 8 : TP0 >= 4 ? 4 : TP0 >= 2 ? 2 : 1;
-    constexpr int DPT = HD / TP;   // dims per thread
-    __shared__ __attribute__((aligned(16))) uint16_t kt[kAttKeys][HD];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kAttKeys][HD];
-    const int tid = threadIdx.x;
-    const int pair = tid / TP, part = tid % TP;
-    const bool active = pair < PAIRS;
-    const int rr = pair / G, g = pair % G;
+    constexpr int RB = G >= 4 ? 1 : 4 / G;     // 16-row blocks per workgroup
+    constexpr int NT = RB * G;                  // tiles
+    constexpr int TPW = (NT + 3) / 4;           // tiles per wave
+    constexpr int NC = HD / 32;                 // 32-dim chunks of q.k
+    constexpr int ND = HD / 16;                 // 16-dim blocks of the output
+    constexpr int KLD = HD + 8;                 // K tile row, halves
+    constexpr int VLD = kAttKeys + 4;           // V^T row, halves (8-byte aligned rows)
+    constexpr int CPR = HD / 8;                 // 16-byte chunks per cache row
+    constexpr int KCH = kAttKeys * CPR / 256;   // K chunks per thread per tile
+    constexpr int VIT = (kAttKeys / 2) * CPR;   // V (key pair, chunk) items per tile
+    __shared__ __attribute__((aligned(16))) _Float16 ks[kAttKeys][KLD];
+    __shared__ __attribute__((aligned(16))) _Float16 vts[HD][VLD];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int qn = lane & 15, j = lane >> 4;
     const int kvh = blockIdx.y;
-    const int r = blockIdx.x * kAttRows + rr;
-    const bool row_ok = active && r < p.m;
-    const int qpos = p.pos0 + r;
-    const int last_pos = p.pos0 + min(p.m - 1, blockIdx.x * kAttRows + kAttRows - 1);
-    const float scale = 1.0f / sqrtf((float)HD);
-    float q[DPT], o[DPT];
-    const int qh = kvh * G + g;
+    const int row0 = blockIdx.x * 16 * RB;
+    const int last_pos = p.pos0 + min(p.m, row0 + 16 * RB) - 1;
+    const int ldq = p.hq * HD;
+    const float qscale = 1.44269504088896341f / sqrtf((float)HD);
+
+    h8_t qb[TPW][NC];
+    f4_t acc[TPW][ND];
+    float mrun[TPW], lrun[TPW];
 #pragma unroll
-    for (int i = 0; i < DPT; i++) {
-        q[i] = row_ok ? p.qout[(size_t)r * p.hq * HD + qh * HD + part * DPT + i] * scale : 0.f;
-        o[i] = 0.f;
-    }
-    float mx = -INFINITY, l = 0.f;
-    for (int t0 = 0; t0 <= last_pos; t0 += kAttKeys) {
-        __syncthreads();
-        for (int idx = tid; idx < kAttKeys * HD / 8; idx += 256) {
-            const int t = idx / (HD / 8), c = idx % (HD / 8);
-            const int pos = t0 + t;
-            u4v_t kv = u4v_t{0u, 0u, 0u, 0u}, vv = u4v_t{0u, 0u, 0u, 0u};
-            if (pos <= last_pos) {
-                const int page = p.pages[pos / kPageTokens];
-                const size_t off = ((size_t)(page * p.hkv + kvh) * kPageTokens + pos % kPageTokens) * HD + c * 8;
-                kv = *reinterpret_cast<const u4v_t*>(p.kcache + off);
-                vv = *reinterpret_cast<const u4v_t*>(p.vcache + off);
+    for (int t = 0; t < TPW; t++) {
+        const int tile = wave + 4 * t, rb = tile / G, h = tile % G;
+        const int r = row0 + rb * 16 + qn;
+        const bool ok = tile < NT && r < p.m;
+        const float* q = p.qout + (size_t)r * ldq + (kvh * G + h) * HD + 8 * j;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float4 lo = float4{0.f, 0.f, 0.f, 0.f}, hi = lo;
+            if (ok) {
+                lo = *reinterpret_cast<const float4*>(q + 32 * c);
+                hi = *reinterpret_cast<const float4*>(q + 32 * c + 4);
             }
-            *reinterpret_cast<u4v_t*>(&kt[t][c * 8]) = kv;
-            *reinterpret_cast<u4v_t*>(&vt[t][c * 8]) = vv;
+            qb[t][c] = h8_t{(_Float16)(lo.x * qscale), (_Float16)(lo.y * qscale), (_Float16)(lo.z * qscale),
+                            (_Float16)(lo.w * qscale), (_Float16)(hi.x * qscale), (_Float16)(hi.y * qscale),
+                            (_Float16)(hi.z * qscale), (_Float16)(hi.w * qscale)};
         }
-        __syncthreads();
-        float s[kAttKeys];
 #pragma unroll
-        for (int t = 0; t < kAttKeys; t++) {
-            float a = 0.f;
-#pragma unroll
-            for (int i = 0; i < DPT; i++) a = fmaf(q[i], kv_val(kt[t][part * DPT + i], p.kv_f16), a);
-#pragma unroll
-            for (int o2 = 1; o2 < TP; o2 <<= 1) a += __shfl_xor(a, o2);
-            s[t] = (t0 + t <= qpos) ? a : -INFINITY;
-        }
-        float tm = mx;
-#pragma unroll
-        for (int t = 0; t < kAttKeys; t++) tm = fmaxf(tm, s[t]);
-        if (tm == -INFINITY) continue;   // no visible key in this tile for this row (uniform per pair)
-        const float corr = expf(mx - tm);
-        l *= corr;
-#pragma unroll
-        for (int i = 0; i < DPT; i++) o[i] *= corr;
-#pragma unroll
-        for (int t = 0; t < kAttKeys; t++) {
-            const float pt = expf(s[t] - tm);
-            l += pt;
-#pragma unroll
-            for (int i = 0; i < DPT; i++) o[i] = fmaf(pt, kv_val(vt[t][part * DPT + i], p.kv_f16), o[i]);
-        }
-        mx = tm;
+        for (int d = 0; d < ND; d++) acc[t][d] = f4_t{0.f, 0.f, 0.f, 0.f};
+        mrun[t] = -INFINITY;
+        lrun[t] = 0.f;
     }
-    if (!row_ok) return;
-    const float il = 1.0f / l;
+
+    // cache tile in registers: K chunks, and V as key pairs for the transposed store
+    u4v_t kr[KCH], vr[2];
+    auto cache_off = [&](int pos, int c8) {
+        const int page = p.pages[pos / kPageTokens];
+        return ((size_t)(page * p.hkv + kvh) * kPageTokens + pos % kPageTokens) * HD + c8 * 8;
+    };
+    auto load_tile = [&](int t0) {
 #pragma unroll
-    for (int i = 0; i < DPT; i++)
-        p.attn16[(size_t)r * p.hq * HD + qh * HD + part * DPT + i] = f2h_bits(o[i] * il);
+        for (int e = 0; e < KCH; e++) {
+            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR, pos = t0 + key;
+            kr[e] = pos <= last_pos ? *reinterpret_cast<const u4v_t*>(p.kcache + cache_off(pos, c8)) : u4v_t{0u, 0u, 0u, 0u};
+        }
+        if (tid < VIT) {
+            const int kp = tid / CPR, c8 = tid % CPR;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int pos = t0 + 2 * kp + e;
+                vr[e] = pos <= last_pos ? *reinterpret_cast<const u4v_t*>(p.vcache + cache_off(pos, c8)) : u4v_t{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    // bfloat16 pair (one dword) -> binary16 pair
+    auto to_f16x2 = [](uint32_t w) -> uint32_t {
+        if constexpr (F16KV) return w;
+        const _Float16 a = (_Float16)__uint_as_float(w << 16), b = (_Float16)__uint_as_float(w & 0xffff0000u);
+        return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int e = 0; e < KCH; e++) {
+            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR;
+            *reinterpret_cast<u4v_t*>(&ks[key][c8 * 8]) =
+                u4v_t{to_f16x2(kr[e].x), to_f16x2(kr[e].y), to_f16x2(kr[e].z), to_f16x2(kr[e].w)};
+        }
+        if (tid < VIT) {
+            const int kp = tid / CPR, c8 = tid % CPR;
+            const uint32_t a[4] = {to_f16x2(vr[0].x), to_f16x2(vr[0].y), to_f16x2(vr[0].z), to_f16x2(vr[0].w)};
+            const uint32_t b[4] = {to_f16x2(vr[1].x), to_f16x2(vr[1].y), to_f16x2(vr[1].z), to_f16x2(vr[1].w)};
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                const uint32_t lo = (a[d / 2] >> (16 * (d & 1))) & 0xffffu, hi = (b[d / 2] >> (16 * (d & 1))) & 0xffffu;
+                *reinterpret_cast<uint32_t*>(&vts[c8 * 8 + d][2 * kp]) = lo | (hi << 16);
+            }
+        }
+    };
+
+    load_tile(0);
+    for (int t0 = 0; t0 <= last_pos; t0 += kAttKeys) {
+        __syncthreads();   // the previous tile is consumed
+        store_tile();
+        __syncthreads();
+        if (t0 + kAttKeys <= last_pos) load_tile(t0 + kAttKeys);
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            const int tile = wave + 4 * t, rb = tile / G;
+            // wave-uniform: an absent tile, or a row block whose rows all precede the keys
+            if (tile >= NT || t0 > p.pos0 + row0 + rb * 16 + 15) continue;
+            const int qpos = p.pos0 + row0 + rb * 16 + qn;
+            f4_t s[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++)
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const h8_t a = *reinterpret_cast<const h8_t*>(&ks[16 * blk + qn][32 * c + 8 * j]);
+                    s[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[t][c], s[blk], 0, 0, 0);
+                }
+            // s[blk][i] = S^T[key t0 + 16 blk + 4 j + i][query qn] (log2 domain)
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (t0 + 16 * blk + 4 * j + i > qpos) s[blk][i] = -INFINITY;
+                    tmax = fmaxf(tmax, s[blk][i]);
+                }
+            tmax = xor32_max(xor16_max(tmax));
+            const float mnew = fmaxf(mrun[t], tmax);
+            const float corr = exp2f(mrun[t] - mnew);
+            float psum = 0.f;
+            _Float16 ph[8];
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float pv = exp2f(s[blk][i] - mnew);
+                    psum += pv;
+                    ph[4 * blk + i] = (_Float16)pv;
+                }
+            psum = xor32_sum(xor16_sum(psum));
+            lrun[t] = lrun[t] * corr + psum;
+            mrun[t] = mnew;
+            const h8_t pb = h8_t{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                acc[t][d] *= corr;
+                const uint2 lo = *reinterpret_cast<const uint2*>(&vts[16 * d + qn][4 * j]);
+                const uint2 hi = *reinterpret_cast<const uint2*>(&vts[16 * d + qn][16 + 4 * j]);
+                const h8_t a = __builtin_bit_cast(h8_t, u4v_t{lo.x, lo.y, hi.x, hi.y});
+                acc[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, acc[t][d], 0, 0, 0);
+            }
+        }
+    }
+    // acc[t][d][i] = O^T[dim 16 d + 4 j + i][query qn]
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const int tile = wave + 4 * t, rb = tile / G, h = tile % G;
+        const int r = row0 + rb * 16 + qn;
+        if (tile >= NT || r >= p.m) continue;
+        const float il = 1.0f / lrun[t];
+        uint16_t* out = p.attn16 + (size_t)r * ldq + (kvh * G + h) * HD + 4 * j;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            const uint32_t w0 = f2h_bits(acc[t][d][0] * il) | ((uint32_t)f2h_bits(acc[t][d][1] * il) << 16);
+            const uint32_t w1 = f2h_bits(acc[t][d][2] * il) | ((uint32_t)f2h_bits(acc[t][d][3] * il) << 16);
+            *reinterpret_cast<uint2*>(out + 16 * d) = uint2{w0, w1};
+        }
+    }
 }
 
 // act16[r][j] = f16(silu(gu[r][j]) * gu[r][F + j]) (silu_mul, model_ops.rs:318-330)
@@ -473,18 +571,28 @@ __global__ void set_pos_kernel(SeqState* s, int pos) {
     if (threadIdx.x == 0) s->pos = pos;
 }
 
+template <int HD, int G>
+hipError_t attention_launch_prefill(const PrefillRows& p, hipStream_t st) {
+    constexpr int RB = G >= 4 ? 1 : 4 / G;
+    const dim3 grid((p.m + 16 * RB - 1) / (16 * RB), p.hkv);
+    if (p.kv_f16) prefill_attention_kernel<HD, G, true><<<grid, 256, 0, st>>>(p);
+    else prefill_attention_kernel<HD, G, false><<<grid, 256, 0, st>>>(p);
+    return hipGetLastError();
+}
+
 template <int HD>
 hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
-    const dim3 grid((p.m + kAttRows - 1) / kAttRows, p.hkv);
     switch (p.hq / p.hkv) {
-    case 1: prefill_attention_kernel<HD, 1><<<grid, 256, 0, st>>>(p); break;
-    case 2: prefill_attention_kernel<HD, 2><<<grid, 256, 0, st>>>(p); break;
-    case 4: prefill_attention_kernel<HD, 4><<<grid, 256, 0, st>>>(p); break;
-    case 7: prefill_attention_kernel<HD, 7><<<grid, 256, 0, st>>>(p); break;
-    case 8: prefill_attention_kernel<HD, 8><<<grid, 256, 0, st>>>(p); break;
+    case 1: return attention_launch_prefill<HD, 1>(p, st);
+    case 2: return attention_launch_prefill<HD, 2>(p, st);
+    case 3: return attention_launch_prefill<HD, 3>(p, st);
+    case 4: return attention_launch_prefill<HD, 4>(p, st);
+    case 5: return attention_launch_prefill<HD, 5>(p, st);
+    case 6: return attention_launch_prefill<HD, 6>(p, st);
+    case 7: return attention_launch_prefill<HD, 7>(p, st);
+    case 8: return attention_launch_prefill<HD, 8>(p, st);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace
