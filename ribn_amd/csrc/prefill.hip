@@ -39,124 +39,165 @@ __device__ __forceinline__ uint16_t f2h_bits(float f) { return __half_as_ushort(
 // values [128 kt + 64 q, +64) of the row (kt = 128-wide K tile, q = quarter of
 // it), computed exactly as dequantize_block (gguf/src/lib.rs:584-649) and then
 // rounded to binary16.
+// The bytes of one quarter are fetched into registers one K tile ahead
+// (QuarterRaw<T>::fetch) and converted into LDS when that tile is staged
+// (QuarterRaw<T>::convert), so the weight loads are in flight during the MFMA
+// phase of the previous tile.
 template <int T>
-__device__ __forceinline__ void deq_quarter(const QMat& w, size_t row, int kt, int q, uint16_t* dst);
+struct QuarterRaw;
 
 __device__ __forceinline__ void store16(uint16_t* dst, const uint32_t (&o)[8]) {
     u4v_t* out = reinterpret_cast<u4v_t*>(dst);
     out[0] = u4v_t{o[0], o[1], o[2], o[3]};
     out[1] = u4v_t{o[4], o[5], o[6], o[7]};
 }
+__device__ __forceinline__ uint32_t lane_of(const u4v_t& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
 
 template <>
-__device__ __forceinline__ void deq_quarter<12>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
+struct QuarterRaw<12> {
     // group pair p = 2 (kt % 2) + q of block kt / 2: group 2p = low nibbles of qs
     // bytes 32p..32p+31, group 2p+1 = their high nibbles; scale dword p holds
     // sc(2p), sc(2p+1), m(2p), m(2p+1)
-    const size_t bi = row * w.nb + (kt >> 1);
-    const int p = 2 * (kt & 1) + q;
-    const uint32_t dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
-    const float d = canon(dd), dmin = canon(dd >> 16);
-    const uint32_t s = reinterpret_cast<const uint32_t*>(w.b + bi * 16)[p];
-    const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
-    const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
-    const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p);
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-        const u4v_t qv = qs[c];
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t v = j == 0 ? qv.x : j == 1 ? qv.y : j == 2 ? qv.z : qv.w;
-            uint32_t a[4], bb[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                a[e] = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> (8 * e)) & 15u)), m0));
-                bb[e] = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> (8 * e + 4)) & 15u)), m1));
-            }
-            lo[2 * j] = a[0] | (a[1] << 16);
-            lo[2 * j + 1] = a[2] | (a[3] << 16);
-            hi[2 * j] = bb[0] | (bb[1] << 16);
-            hi[2 * j + 1] = bb[2] | (bb[3] << 16);
-        }
-        store16(dst + 16 * c, lo);
-        store16(dst + 32 + 16 * c, hi);
+    uint32_t dd, s;
+    u4v_t qv[2];
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int q) {
+        const size_t bi = row * w.nb + (kt >> 1);
+        const int p = 2 * (kt & 1) + q;
+        dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
+        s = reinterpret_cast<const uint32_t*>(w.b + bi * 16)[p];
+        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p);
+        qv[0] = qs[0];
+        qv[1] = qs[1];
     }
-}
+    __device__ __forceinline__ void convert(uint16_t* dst) const {
+        const float d = canon(dd), dmin = canon(dd >> 16);
+        const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
+        const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v = lane_of(qv[c], j);
+                uint32_t a[4], bb[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    a[e] = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> (8 * e)) & 15u)), m0));
+                    bb[e] = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> (8 * e + 4)) & 15u)), m1));
+                }
+                lo[2 * j] = a[0] | (a[1] << 16);
+                lo[2 * j + 1] = a[2] | (a[3] << 16);
+                hi[2 * j] = bb[0] | (bb[1] << 16);
+                hi[2 * j + 1] = bb[2] | (bb[3] << 16);
+            }
+            store16(dst + 16 * c, lo);
+            store16(dst + 32 + 16 * c, hi);
+        }
+    }
+};
 
 template <>
-__device__ __forceinline__ void deq_quarter<14>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
+struct QuarterRaw<14> {
     // chunk h = kt % 2 of block kt / 2 (ql bytes 64h.., qh bytes 32h..); value
     // 32v + l of the chunk: ((ql[32 (v%2) + l] >> 4 (v/2)) & 15) | (((qh[l] >> 2v) & 3) << 4),
     // minus 32, times d * sc(8h + 2v + l/16); the quarter q holds v = 2q, 2q + 1.
     // Sub-block scale s sits at c-plane byte 2c + slot, c = 4 (s/8) + s%4, slot = (s/4) % 2.
-    const size_t bi = row * w.nb + (kt >> 1);
-    const int h = kt & 1;
-    const float d = canon(*reinterpret_cast<const uint16_t*>(w.d + bi * 2));
-    const uint8_t* sp = w.c + bi * 16;
-    const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * h);
-    const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(w.b + bi * 64 + 32 * h);
+    uint32_t d16, sc4;   // d; the quarter's four sub-block scales (int8, order vv * 2 + lc)
+    int q;
+    u4v_t ql[4], qh[2];
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int qq) {
+        const size_t bi = row * w.nb + (kt >> 1);
+        const int h = kt & 1;
+        q = qq;
+        d16 = *reinterpret_cast<const uint16_t*>(w.d + bi * 2);
+        const uint8_t* sp = w.c + bi * 16;
+        sc4 = 0;
 #pragma unroll
-    for (int vv = 0; vv < 2; vv++) {
-        const int v = 2 * q + vv;
+        for (int vv = 0; vv < 2; vv++)
 #pragma unroll
-        for (int lc = 0; lc < 2; lc++) {
-            const int sb = 8 * h + 2 * v + lc;
-            const float gsc = __fmul_rn(d, (float)(int8_t)sp[2 * (4 * (sb / 8) + sb % 4) + (sb / 4) % 2]);
-            const u4v_t qlv = ql4[2 * vv + lc], qhv = qh4[lc];
-            uint32_t o[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t lw = j == 0 ? qlv.x : j == 1 ? qlv.y : j == 2 ? qlv.z : qlv.w;
-                const uint32_t hw = j == 0 ? qhv.x : j == 1 ? qhv.y : j == 2 ? qhv.z : qhv.w;
-                uint32_t e[4];
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int qq = (int)((((lw >> (8 * b)) >> (4 * q)) & 15u) | ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
-                    e[b] = f2h_bits(__fmul_rn(gsc, (float)qq));
-                }
-                o[2 * j] = e[0] | (e[1] << 16);
-                o[2 * j + 1] = e[2] | (e[3] << 16);
+            for (int lc = 0; lc < 2; lc++) {
+                const int sb = 8 * h + 2 * (2 * qq + vv) + lc;
+                sc4 |= (uint32_t)sp[2 * (4 * (sb / 8) + sb % 4) + (sb / 4) % 2] << (8 * (2 * vv + lc));
             }
-            store16(dst + 32 * vv + 16 * lc, o);
-        }
+        const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * h);
+        const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(w.b + bi * 64 + 32 * h);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ql[i] = ql4[i];
+        qh[0] = qh4[0];
+        qh[1] = qh4[1];
     }
-}
-
-template <>
-__device__ __forceinline__ void deq_quarter<8>(const QMat& w, size_t row, int kt, int q, uint16_t* dst) {
-    // Q8_0 blocks 4 kt + 2q and 4 kt + 2q + 1; past the row's end (k % 128 != 0): zeros
+    __device__ __forceinline__ void convert(uint16_t* dst) const {
+        const float d = canon(d16);
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-        const int qb = 4 * kt + 2 * q + b;
-        uint32_t o[2][8];
-        if (qb >= (int)w.nb) {
+        for (int vv = 0; vv < 2; vv++) {
+            const int v = 2 * q + vv;
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) o[c][j] = 0u;
-        } else {
-            const size_t bi = row * w.nb + (size_t)qb;
-            const float d = canon(*reinterpret_cast<const uint16_t*>(w.b + bi * 2));
-            const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const u4v_t qv = qs[c];
+            for (int lc = 0; lc < 2; lc++) {
+                const float gsc = __fmul_rn(d, (float)(int8_t)(sc4 >> (8 * (2 * vv + lc))));
+                const u4v_t qlv = ql[2 * vv + lc], qhv = qh[lc];
+                uint32_t o[8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint32_t v = j == 0 ? qv.x : j == 1 ? qv.y : j == 2 ? qv.z : qv.w;
+                    const uint32_t lw = lane_of(qlv, j), hw = lane_of(qhv, j);
                     uint32_t e[4];
 #pragma unroll
-                    for (int k = 0; k < 4; k++) e[k] = f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k))));
+                    for (int b = 0; b < 4; b++) {
+                        const int qq = (int)((((lw >> (8 * b)) >> (4 * q)) & 15u) | ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
+                        e[b] = f2h_bits(__fmul_rn(gsc, (float)qq));
+                    }
+                    o[2 * j] = e[0] | (e[1] << 16);
+                    o[2 * j + 1] = e[2] | (e[3] << 16);
+                }
+                store16(dst + 32 * vv + 16 * lc, o);
+            }
+        }
+    }
+};
+
+template <>
+struct QuarterRaw<8> {
+    // Q8_0 blocks 4 kt + 2q and 4 kt + 2q + 1; past the row's end (k % 128 != 0): zeros
+    uint32_t d16[2];
+    u4v_t qv[2][2];
+    bool present[2];
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int q) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int qb = 4 * kt + 2 * q + b;
+            present[b] = qb < (int)w.nb;
+            d16[b] = 0u;
+            qv[b][0] = qv[b][1] = u4v_t{0u, 0u, 0u, 0u};
+            if (present[b]) {
+                const size_t bi = row * w.nb + (size_t)qb;
+                d16[b] = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
+                const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
+                qv[b][0] = qs[0];
+                qv[b][1] = qs[1];
+            }
+        }
+    }
+    __device__ __forceinline__ void convert(uint16_t* dst) const {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            uint32_t o[2][8];
+            const float d = canon(d16[b]);
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t v = lane_of(qv[b][c], j);
+                    uint32_t e[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) e[k] = present[b] ? f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k)))) : 0u;
                     o[c][2 * j] = e[0] | (e[1] << 16);
                     o[c][2 * j + 1] = e[2] | (e[3] << 16);
                 }
             }
+            store16(dst + 32 * b, o[0]);
+            store16(dst + 32 * b + 16, o[1]);
         }
-        store16(dst + 32 * b, o[0]);
-        store16(dst + 32 * b + 16, o[1]);
     }
-}
+};
 
 // Workgroup tile: 128 chunk rows x 128 weight rows of one segment; wave w owns
 // weight rows 32w..32w+31 of the tile (two 16-column MFMA blocks) for all 128
@@ -188,21 +229,44 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
     const int wr = tid >> 1, wq = tid & 1;   // dequant: row of the tile, quarter of the K tile
     const size_t wrow = (size_t)min(n0 + wr, n_rows - 1);
-    for (int kt = kt0; kt < kt1; kt++) {
-        __syncthreads();
-        // X slice: 128 rows x 128 halves = 2048 16-byte chunks, 8 per thread
+    const bool use_b = si == 2 && TB != TA;
+    // next tile in registers: X slice (128 rows x 128 halves = 2048 16-byte
+    // chunks, 8 per thread) and this thread's weight quarter
+    u4v_t xr[8];
+    QuarterRaw<TA> ra;
+    QuarterRaw<TB> rb;
+    auto fetch = [&](int kt) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int idx = j * kGemmThreads + tid;
             const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
-            u4v_t v = u4v_t{0u, 0u, 0u, 0u};
-            if (m0 + r < g.m && col < g.k) v = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
-            *reinterpret_cast<u4v_t*>(xs + r * kLdsRow + c * 8) = v;
+            xr[j] = u4v_t{0u, 0u, 0u, 0u};
+            if (m0 + r < g.m && col < g.k) xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
         }
-        if (si == 2 && TB != TA) deq_quarter<TB>(sg.w, wrow, kt, wq, ws + wr * kLdsRow + 64 * wq);
-        else deq_quarter<TA>(sg.w, wrow, kt, wq, ws + wr * kLdsRow + 64 * wq);
+        if constexpr (TB != TA) {
+            if (use_b) rb.fetch(sg.w, wrow, kt, wq);
+            else ra.fetch(sg.w, wrow, kt, wq);
+        } else {
+            ra.fetch(sg.w, wrow, kt, wq);
+        }
+    };
+    if (kt0 < kt1) fetch(kt0);
+    for (int kt = kt0; kt < kt1; kt++) {
+        __syncthreads();   // the previous tile's MFMA reads are done
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int idx = j * kGemmThreads + tid;
+            *reinterpret_cast<u4v_t*>(xs + (idx >> 4) * kLdsRow + (idx & 15) * 8) = xr[j];
+        }
+        if constexpr (TB != TA) {
+            if (use_b) rb.convert(ws + wr * kLdsRow + 64 * wq);
+            else ra.convert(ws + wr * kLdsRow + 64 * wq);
+        } else {
+            ra.convert(ws + wr * kLdsRow + 64 * wq);
+        }
         __syncthreads();
+        if (kt + 1 < kt1) fetch(kt + 1);
 #pragma unroll
         for (int ks = 0; ks < kTileK / 32; ks++) {
             const int kk = ks * 32 + 8 * (lane >> 4);
