@@ -61,10 +61,10 @@ typedef struct {
 /* KV cache in bfloat16 instead of the default binary16 (binary16 is the reference
  * CUDA cache type, kv_append_f16 nvidia/src/model_ops.rs:1258-1276). */
 #define RIBN_LOAD_KV_BF16 1u
-/* Run each token step as the chain of per-stage kernel launches (HIP graphs)
- * instead of the persistent one-launch step kernel. The persistent kernel is
- * used by default when one is compiled for the model's configuration. */
-#define RIBN_LOAD_LAUNCH_CHAIN 2u
+/* Run each token step as one persistent kernel launch (grid barriers between the
+ * stages) when one is compiled for the model's configuration, instead of the
+ * default chain of per-stage launches replayed as HIP graphs. */
+#define RIBN_LOAD_PERSISTENT_STEP 2u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);

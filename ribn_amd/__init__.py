@@ -32,7 +32,7 @@ BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (25
 
 RIBN_OK, RIBN_PENDING = 0, 1
 LOAD_KV_BF16 = 1
-LOAD_LAUNCH_CHAIN = 2
+LOAD_PERSISTENT_STEP = 2
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -285,7 +285,7 @@ class QwenRocm:
         if step not in ("persistent", "chain"):
             raise ValueError("step must be 'persistent' or 'chain'")
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
-                           (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_LAUNCH_CHAIN if step == "chain" else 0))
+                           (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()

@@ -983,7 +983,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     for (int s = (int)M->max_seqs - 1; s >= 0; s--) M->free_slots.push_back(s);
     for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
     build_launches(M);
-    HIPCHK(build_step(M, (o.flags & RIBN_LOAD_LAUNCH_CHAIN) == 0));
+    HIPCHK(build_step(M, (o.flags & RIBN_LOAD_PERSISTENT_STEP) != 0));
     *out = Mp.release();
     return RIBN_OK;
 }
