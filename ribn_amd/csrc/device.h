@@ -196,8 +196,8 @@ __device__ __forceinline__ void stage_pre(const float* x, const float* norm_w, i
 // group sum into gs; ss gathers the sum of squares of x. All lanes take part
 // (the block maximum is a quad reduction).
 template <int T>
-__device__ __forceinline__ void stage_group(int g, int k, const float4 (&xv)[4], const float4* wv, int8_t* xs,
-                                            float* gs, float& ss) {
+__device__ __forceinline__ void stage_group(int g, int k, const float4 (&xv)[4], const float4 (&wv)[4], bool norm,
+                                            int8_t* xs, float* gs, float& ss) {
     const int n_units = T == 8 ? k / 16 : k / 32;
     const bool valid = g < k / 16;
     u4_t* planes = reinterpret_cast<u4_t*>(xs);
@@ -206,7 +206,7 @@ __device__ __forceinline__ void stage_group(int g, int k, const float4 (&xv)[4],
     for (int j = 0; j < 4; j++) {
         float4 t = valid ? xv[j] : float4{0.f, 0.f, 0.f, 0.f};
         ss += t.x * t.x + t.y * t.y + t.z * t.z + t.w * t.w;
-        if (wv && valid) {
+        if (norm && valid) {
             const float4 w = wv[j];
             t.x *= w.x; t.y *= w.y; t.z *= w.z; t.w *= w.w;
         }
@@ -259,7 +259,7 @@ __device__ __forceinline__ void stage_group(int g, int k, const float4 (&xv)[4],
 // epilogue applies to the row sums. The first NP passes take their input from
 // `pre` (loaded by stage_pre).
 template <int T, int NP = 0>
-__device__ float stage_x(const float* x, const float* norm_w, float eps, int k, int8_t* xs, float* gs, float* red,
+__device__ __forceinline__ float stage_x(const float* x, const float* norm_w, float eps, int k, int8_t* xs, float* gs, float* red,
                          const XPre<NP == 0 ? 1 : NP>* pre = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -274,11 +274,10 @@ __device__ float stage_x(const float* x, const float* norm_w, float eps, int k, 
         const int g = q * kThreads + tid;
         if (q * kThreads < n16) {   // uniform
             float4 wl[4];
-            if (norm && q > 0) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) wl[j] = g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
-            }
-            stage_group<T>(g, k, pre->x[q], norm ? (q == 0 ? pre->w : wl) : nullptr, xs, gs, ss);
+            for (int j = 0; j < 4; j++)
+                wl[j] = q == 0 ? pre->w[j] : norm && g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
+            stage_group<T>(g, k, pre->x[q], wl, norm, xs, gs, ss);
         }
     }
     for (int base = NP * kThreads; base < n16; base += kThreads) {
@@ -287,9 +286,9 @@ __device__ float stage_x(const float* x, const float* norm_w, float eps, int k, 
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             xl[j] = g < n16 ? x4[g * 4 + j] : float4{0.f, 0.f, 0.f, 0.f};
-            if (norm) wl[j] = g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
+            wl[j] = norm && g < n16 ? w4[g * 4 + j] : float4{1.f, 1.f, 1.f, 1.f};
         }
-        stage_group<T>(g, k, xl, norm ? wl : nullptr, xs, gs, ss);
+        stage_group<T>(g, k, xl, wl, norm, xs, gs, ss);
     }
     float inv = 1.0f;
     if (norm) {
@@ -507,14 +506,14 @@ __device__ __forceinline__ void mv_finish(const MvSeg& sg, const WaveWork& w, co
                                           float oscale, float addend, uint64_t& best) {
     if (c.gi != w.ngr - 1) return;
     const int lane = threadIdx.x & 63;
-    // both row sums in one reduction: after the xor-32 step lanes 0-31 hold
-    // row a, lanes 32-63 row b
-    const bool lo_half = lane < 32;
-    const float send = lo_half ? b0 : a0;
-    float v = (lo_half ? a0 : b0) + __shfl_xor(send, 32);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    const float ya = __shfl(v, 0) * oscale, yb = __shfl(v, 32) * oscale;
+    // both row sums in one reduction: the permlane32 swap of (a0, b0) leaves
+    // {a0[l], a0[l + 32]} in lanes 0-31 and {b0[l - 32], b0[l]} in lanes 32-63,
+    // then DPP sums within each half
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0), __float_as_uint(b0), false, false);
+    float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    v = xor16_sum(group_sum<16>(v));
+    const float ya = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) * oscale;
+    const float yb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) * oscale;
     a0 = b0 = 0.f;
     const int item = w.first_item + c.it * kWaves;
     const int ra = w.pair ? item : 2 * item;
