@@ -73,6 +73,33 @@ def cpu_baseline(path, info):
                       f"{secs:.1f} s single-threaded; tok/s = host GB/s / weight bytes per token"}
 
 
+def gemma_cpu_baseline():
+    """the Gemma 4 host CPU BF16 decoder restatement (oracle/gemma4.c, restating
+    crates/gemma4/src/cpu/) on the tiny random-init model, 64-token prompt then 32 greedy tokens,
+    single-threaded as the reference's CPU path is."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import gemma_oracle as g4
+    c = g4.config()
+    w, keep = g4.synth_weights(c, seed=0)
+    prompt = np.random.default_rng(0).integers(0, c.vocab, 64).tolist()
+    d = g4.Gemma4Oracle(c, w)
+    t0 = time.perf_counter()
+    lg = d.prefill(prompt)
+    t1 = time.perf_counter()
+    toks = [d.argmax(lg)]
+    for _ in range(31):
+        toks.append(d.argmax(d.decode(toks[-1])))
+    t2 = time.perf_counter()
+    d.close()
+    decode_ms = (t2 - t1) * 1e3 / 31
+    return {"value": round(1e3 / decode_ms, 3), "unit": "tok/s (configs[0] decode)", "cores": 1, "kind": "port",
+            "prefill_ms_per_token": round((t1 - t0) * 1e3 / 64, 3), "decode_ms_per_token": round(decode_ms, 3),
+            "sample": "Gemma 4 CPU BF16 decoder restatement, tiny config (hidden 512, 4 layers, 8/2 heads x 64, "
+                      "FFN 2048, vocab 32000), 64-token prompt + 32 greedy tokens, single-threaded",
+            "first_tokens": toks[:8]}
+
+
 def probe_traffic():
     """Launch sequence measured by the FETCH_SIZE / WRITE_SIZE passes: 20 replays each of the layer-0 gate/up,
     ffn_down and head matvecs (same kernels and shapes as the 36-layer model), then 5 copies of 1 GiB between
@@ -166,6 +193,7 @@ def main():
         step_gbs = step_bytes / (ms_per_step / 1e3) / 1e9
         m.close()
         cpu = None if args.no_cpu else cpu_baseline(path, info)
+        cpu_gemma = None if args.no_cpu else gemma_cpu_baseline()
     finally:
         if made and os.path.exists(path):
             os.unlink(path)
@@ -201,6 +229,7 @@ def main():
                        "down_gbs": round(down_bytes / down_ms / 1e6, 1), "head_q6k": round(head_ms * 1e3, 2),
                        "head_gbs": round(head_bytes / head_ms / 1e6, 1)},
         "cpu_baseline": cpu,
+        "cpu_baseline_configs0": cpu_gemma,
         "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)},
     }
     print(json.dumps(out))
