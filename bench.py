@@ -100,6 +100,44 @@ def gemma_cpu_baseline():
             "first_tokens": toks[:8]}
 
 
+def gemma_rocm_line():
+    """configs[0] on the GPU behind the GemmaDecode seam (ribn_rocm_gemma_*): the same tiny package as
+    the CPU baseline, 64-token prompt then 32 greedy tokens; decode bytes are every projection matrix
+    streamed once per token (BF16) plus the tied head."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import gemma_oracle as g4
+    import ribn_amd
+    c = g4.config()
+    kinds = ("S", "S", "S", "F")
+    named = g4.synth_named(c, seed=0)
+    d = tempfile.mkdtemp(prefix="ribn_gemma_")
+    try:
+        g4.write_package(d, c, named, kinds)
+        prompt = np.random.default_rng(0).integers(0, c.vocab, 64).tolist()
+        with ribn_amd.GemmaRocm(d) as m:
+            m.prefill(prompt)   # warm
+            m.reset()
+            t0 = time.perf_counter()
+            lg = m.prefill(prompt)
+            t1 = time.perf_counter()
+            toks = [m.argmax(lg)]
+            for _ in range(31):
+                toks.append(m.argmax(m.decode(toks[-1])))
+            t2 = time.perf_counter()
+    finally:
+        for f in os.listdir(d):
+            os.unlink(os.path.join(d, f))
+        os.rmdir(d)
+    streamed = sum(a.size for n, a in named.items()
+                   if a.ndim == 2 and not n.endswith("embed_tokens_per_layer.weight")) * 2
+    decode_s = (t2 - t1) / 31
+    return {"decode_tok_s": round(1 / decode_s, 1), "prefill_tok_s": round(64 / (t1 - t0), 1),
+            "decode_ms_per_token": round(decode_s * 1e3, 3), "bytes_per_token": int(streamed),
+            "achieved_gbs": round(streamed / decode_s / 1e9, 1), "first_tokens": toks[:8],
+            "note": "BF16 eager policy, bit-exact with the CPU decoder restatement; sequential FP32 sums per output"}
+
+
 def probe_traffic():
     """Launch sequence measured by the FETCH_SIZE / WRITE_SIZE passes: 20 replays each of the layer-0 gate/up,
     ffn_down and head matvecs (same kernels and shapes as the 36-layer model), then 5 copies of 1 GiB between
@@ -194,6 +232,7 @@ def main():
         m.close()
         cpu = None if args.no_cpu else cpu_baseline(path, info)
         cpu_gemma = None if args.no_cpu else gemma_cpu_baseline()
+        gemma_gpu = gemma_rocm_line()
     finally:
         if made and os.path.exists(path):
             os.unlink(path)
@@ -230,6 +269,7 @@ def main():
                        "head_gbs": round(head_bytes / head_ms / 1e6, 1)},
         "cpu_baseline": cpu,
         "cpu_baseline_configs0": cpu_gemma,
+        "configs0_rocm": gemma_gpu,
         "setup_s": {"synth": round(t_synth, 1), "load": round(t_load, 1)},
     }
     print(json.dumps(out))

@@ -223,6 +223,34 @@ int ribn_rocm_step_stamps(ribn_rocm_model *model, uint32_t ctx, double *out_ns, 
 /* Synthetic model writer (test and benchmark inputs; no reference counterpart:
  * the reference loads real artifacts only). Seeded N(0, weight_std) weights,
  * quantized to GGML blocks, written as GGUF v3. */
+/* ---- Gemma 4 text decoder (the GemmaDecode seam) ------------------------------
+ * Replaces `trait GemmaDecode` (crates/gemma4/src/executor/backend.rs:10-33:
+ * advance_prefill, prefill, decode, position, close) and its loader
+ * TextOwner::load_gemma_cuda (crates/text/src/gemma_load.rs:63-101). The package
+ * directory holds config.json and a single BF16 model.safetensors, checked as
+ * Gemma4Source::open does (crates/gemma4/src/source.rs:56-160). Logits are BF16
+ * bit patterns after the final soft cap, vocab entries. Failed chunks leave
+ * the position unchanged. */
+typedef struct ribn_rocm_gemma ribn_rocm_gemma;
+typedef struct {
+    uint32_t vocab, hidden, layers, context;
+} ribn_rocm_gemma_info_t;
+int ribn_rocm_gemma_open(const char *package_dir, int32_t device, ribn_rocm_gemma **out, char *err, size_t err_len);
+void ribn_rocm_gemma_close(ribn_rocm_gemma *g);
+int ribn_rocm_gemma_info(const ribn_rocm_gemma *g, ribn_rocm_gemma_info_t *out);
+/* prefill (backend.rs:14): process the chunk, write its last token's logits */
+int ribn_rocm_gemma_prefill(ribn_rocm_gemma *g, const uint32_t *tokens, uint32_t n, uint16_t *logits,
+                            char *err, size_t err_len);
+/* advance_prefill (backend.rs:12): process the chunk without the readout */
+int ribn_rocm_gemma_advance_prefill(ribn_rocm_gemma *g, const uint32_t *tokens, uint32_t n, char *err,
+                                    size_t err_len);
+/* decode (backend.rs:16): one token, its logits */
+int ribn_rocm_gemma_decode(ribn_rocm_gemma *g, uint32_t token, uint16_t *logits, char *err, size_t err_len);
+/* position (backend.rs:18) */
+uint32_t ribn_rocm_gemma_position(const ribn_rocm_gemma *g);
+/* Gemma4CpuDecoder::reset (crates/gemma4/src/cpu/decoder.rs:98-105) */
+int ribn_rocm_gemma_reset(ribn_rocm_gemma *g);
+
 typedef struct {
     int32_t qwen3;            /* 1: qwen3 (q/k norm, no bias); 0: qwen2 (q/k/v bias) */
     uint32_t hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab;

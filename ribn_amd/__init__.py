@@ -400,8 +400,89 @@ class QwenRocm:
         return ms.value, nbytes.value
 
 
+# --------------------------------------------------------------------------
+# GemmaDecode mirror (crates/gemma4/src/executor/backend.rs:10-33)
+
+class GemmaInfo(ctypes.Structure):
+    _fields_ = [("vocab", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("layers", ctypes.c_uint32),
+                ("context", ctypes.c_uint32)]
+
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_sig("ribn_rocm_gemma_open", _c.c_int, _c.c_char_p, _c.c_int32, _c.POINTER(_c.c_void_p), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemma_close", None, _c.c_void_p)
+_sig("ribn_rocm_gemma_info", _c.c_int, _c.c_void_p, _c.POINTER(GemmaInfo))
+_sig("ribn_rocm_gemma_prefill", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _u16p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemma_advance_prefill", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemma_decode", _c.c_int, _c.c_void_p, _c.c_uint32, _u16p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemma_position", _c.c_uint32, _c.c_void_p)
+_sig("ribn_rocm_gemma_reset", _c.c_int, _c.c_void_p)
+
+
+class GemmaRocm:
+    """The Gemma 4 text decoder on the GPU behind the GemmaDecode seam: prefill / advance_prefill /
+    decode return or skip the BF16 logits (uint16 bit patterns, post soft cap) of the chunk's last
+    token; a rejected chunk leaves the position unchanged (RibnError)."""
+
+    def __init__(self, package_dir: str, device: int = 0):
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERR)
+        _check(_lib.ribn_rocm_gemma_open(package_dir.encode(), device, ctypes.byref(h), err, _ERR), err)
+        self._h = h
+        info = GemmaInfo()
+        _lib.ribn_rocm_gemma_info(self._h, ctypes.byref(info))
+        self.vocab, self.hidden, self.layers, self.context = info.vocab, info.hidden, info.layers, info.context
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.ribn_rocm_gemma_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def position(self) -> int:
+        return int(_lib.ribn_rocm_gemma_position(self._h))
+
+    def reset(self):
+        _lib.ribn_rocm_gemma_reset(self._h)
+
+    def prefill(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.vocab, np.uint16)
+        err = ctypes.create_string_buffer(_ERR)
+        _check(_lib.ribn_rocm_gemma_prefill(self._h, _ptr(t, _u32p), t.size, _ptr(out, _u16p), err, _ERR), err)
+        return out
+
+    def advance_prefill(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        err = ctypes.create_string_buffer(_ERR)
+        _check(_lib.ribn_rocm_gemma_advance_prefill(self._h, _ptr(t, _u32p), t.size, err, _ERR), err)
+
+    def decode(self, token: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.uint16)
+        err = ctypes.create_string_buffer(_ERR)
+        _check(_lib.ribn_rocm_gemma_decode(self._h, int(token), _ptr(out, _u16p), err, _ERR), err)
+        return out
+
+    @staticmethod
+    def argmax(logits: np.ndarray) -> int:
+        """First maximum of BF16 logits (cpu/decoder.rs:316-332)."""
+        v = (np.asarray(logits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+        if v.size == 0 or np.isnan(v[0]):   # nothing compares greater than a NaN first entry
+            return 0
+        return int(np.argmax(np.where(np.isnan(v), -np.inf, v)))
+
+
 __all__ = [
-    "QwenRocm", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
+    "QwenRocm", "GemmaRocm", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
     "dequantize", "gemv", "bench_gemv", "prefill_gemm", "argmax", "LIB_PATH", "GGML_F32", "GGML_F16", "GGML_Q8_0", "GGML_Q4_K",
     "GGML_Q6_K", "BLOCK", "STEP_PREFILL", "STEP_DECODE", "ADMIT_READY", "ADMIT_REJECTED", "ADMIT_DEFERRED",
 ]

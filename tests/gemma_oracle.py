@@ -18,7 +18,9 @@ reference's parameter order (parameters.rs:106-160) and rounded to BF16. Norm
 weights and layer scalars are 1.0.
 """
 import ctypes
+import json
 import os
+import struct
 
 import numpy as np
 
@@ -123,49 +125,118 @@ def config(vocab=32000, hidden=512, intermediate=2048, heads=8, kv_heads=2, head
     return c
 
 
-def synth_weights(c, seed=0, std=0.02):
-    """Seeded BF16 weights for config c in parameter order; returns (G4Weights, keepalive list)."""
+LAYER_SUFFIX = {"q": "self_attn.q_proj.weight", "k": "self_attn.k_proj.weight", "v": "self_attn.v_proj.weight",
+                "o": "self_attn.o_proj.weight", "q_norm": "self_attn.q_norm.weight",
+                "k_norm": "self_attn.k_norm.weight", "input_norm": "input_layernorm.weight",
+                "post_attention_norm": "post_attention_layernorm.weight",
+                "pre_feedforward_norm": "pre_feedforward_layernorm.weight",
+                "post_feedforward_norm": "post_feedforward_layernorm.weight", "gate": "mlp.gate_proj.weight",
+                "up": "mlp.up_proj.weight", "down": "mlp.down_proj.weight",
+                "ple_gate": "per_layer_input_gate.weight", "ple_projection": "per_layer_projection.weight",
+                "post_ple_norm": "post_per_layer_input_norm.weight", "layer_scalar": "layer_scalar"}
+PREFIX = "model.language_model."
+
+
+def synth_named(c, seed=0, std=0.02):
+    """Seeded BF16 parameters for config c, keyed by checkpoint name, in the reference's parameter
+    order (parameters.rs:106-160): N(0, std) matrices, 1.0 norms and layer scalars."""
     rng = np.random.default_rng(seed)
-    keep = []
+    out = {}
 
-    def normal(*shape):
-        a = bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).reshape(shape)
-        keep.append(a)
-        return ptr(a)
+    def normal(name, *shape):
+        out[PREFIX + name] = bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).reshape(shape)
 
-    def ones(n):
-        a = np.full(n, 0x3F80, np.uint16)
-        keep.append(a)
-        return ptr(a)
+    def ones(name, n):
+        out[PREFIX + name] = np.full(n, 0x3F80, np.uint16)
 
     H, F, P, L = c.hidden, c.intermediate, c.ple, c.layers
-    w = G4Weights()
-    w.embed = normal(c.vocab, H)
-    w.ple_embed = normal(c.ple_vocab, L * P)
-    w.ple_projection = normal(L * P, H)
-    w.ple_norm = ones(P)
-    w.final_norm = ones(H)
+    normal("embed_tokens.weight", c.vocab, H)
+    normal("embed_tokens_per_layer.weight", c.ple_vocab, L * P)
+    normal("per_layer_model_projection.weight", L * P, H)
+    ones("per_layer_projection_norm.weight", P)
+    ones("norm.weight", H)
     for l in range(L):
         hd = c.head_dim[l]
-        lw = w.layer[l]
-        lw.q = normal(c.heads * hd, H)
-        lw.k = normal(c.kv_heads * hd, H)
-        lw.v = normal(c.kv_heads * hd, H)
-        lw.o = normal(H, c.heads * hd)
-        lw.q_norm = ones(hd)
-        lw.k_norm = ones(hd)
-        lw.input_norm = ones(H)
-        lw.post_attention_norm = ones(H)
-        lw.pre_feedforward_norm = ones(H)
-        lw.post_feedforward_norm = ones(H)
-        lw.gate = normal(F, H)
-        lw.up = normal(F, H)
-        lw.down = normal(H, F)
-        lw.ple_gate = normal(P, H)
-        lw.ple_projection = normal(H, P)
-        lw.post_ple_norm = ones(H)
-        lw.layer_scalar = ones(1)
-    return w, keep
+        lp = f"layers.{l}."
+        shapes = {"q": (c.heads * hd, H), "k": (c.kv_heads * hd, H), "v": (c.kv_heads * hd, H),
+                  "o": (H, c.heads * hd), "q_norm": hd, "k_norm": hd, "input_norm": H, "post_attention_norm": H,
+                  "pre_feedforward_norm": H, "post_feedforward_norm": H, "gate": (F, H), "up": (F, H),
+                  "down": (H, F), "ple_gate": (P, H), "ple_projection": (H, P), "post_ple_norm": H,
+                  "layer_scalar": 1}
+        for field in LAYER_FIELDS:
+            shp = shapes[field]
+            if isinstance(shp, tuple):
+                normal(lp + LAYER_SUFFIX[field], *shp)
+            else:
+                ones(lp + LAYER_SUFFIX[field], shp)
+    return out
+
+
+def weights_from_named(c, named):
+    """G4Weights pointing into the named arrays (which must stay alive)."""
+    w = G4Weights()
+    w.embed = ptr(named[PREFIX + "embed_tokens.weight"])
+    w.ple_embed = ptr(named[PREFIX + "embed_tokens_per_layer.weight"])
+    w.ple_projection = ptr(named[PREFIX + "per_layer_model_projection.weight"])
+    w.ple_norm = ptr(named[PREFIX + "per_layer_projection_norm.weight"])
+    w.final_norm = ptr(named[PREFIX + "norm.weight"])
+    for l in range(c.layers):
+        for field in LAYER_FIELDS:
+            setattr(w.layer[l], field, ptr(named[PREFIX + f"layers.{l}." + LAYER_SUFFIX[field]]))
+    return w
+
+
+def synth_weights(c, seed=0, std=0.02):
+    """Seeded BF16 weights for config c; returns (G4Weights, keepalive)."""
+    named = synth_named(c, seed, std)
+    return weights_from_named(c, named), named
+
+
+def config_json(c, layer_kinds, shared=0):
+    """The package's config.json for config c (the fields Gemma4Config::from_json reads)."""
+    kinds = ["full_attention" if k == "F" else "sliding_attention" for k in layer_kinds]
+    local = next((c.head_dim[i] for i in range(c.layers) if not c.kind[i]), c.head_dim[0])
+    glob = next((c.head_dim[i] for i in range(c.layers) if c.kind[i]), c.head_dim[0])
+    tl = next((float(c.theta[i]) for i in range(c.layers) if not c.kind[i]), 1e4)
+    tg = next((float(c.theta[i]) for i in range(c.layers) if c.kind[i]), 1e4)
+    text = {"model_type": "gemma4_text", "dtype": "bfloat16", "attention_bias": False, "attention_dropout": 0.0,
+            "attention_k_eq_v": False, "bos_token_id": 2, "eos_token_id": 1, "pad_token_id": 0,
+            "enable_moe_block": False, "final_logit_softcapping": float(c.softcap), "global_head_dim": glob,
+            "head_dim": local, "hidden_activation": "gelu_pytorch_tanh", "hidden_size": c.hidden,
+            "hidden_size_per_layer_input": c.ple, "initializer_range": 0.02, "intermediate_size": c.intermediate,
+            "layer_types": kinds, "max_position_embeddings": c.context, "num_attention_heads": c.heads,
+            "num_hidden_layers": c.layers, "num_key_value_heads": c.kv_heads, "num_kv_shared_layers": shared,
+            "rms_norm_eps": float(c.eps), "sliding_window": c.window,
+            "rope_parameters": {"sliding_attention": {"rope_type": "default", "rope_theta": tl},
+                                "full_attention": {"rope_type": "proportional", "rope_theta": tg,
+                                                   "partial_rotary_factor": 0.25}},
+            "tie_word_embeddings": True, "use_bidirectional_attention": None, "use_cache": True,
+            "use_double_wide_mlp": False, "vocab_size": c.vocab, "vocab_size_per_layer_input": c.ple_vocab,
+            "num_global_key_value_heads": None}
+    return {"architectures": ["Gemma4ForConditionalGeneration"], "model_type": "gemma4", "dtype": "bfloat16",
+            "tie_word_embeddings": True, "image_token_id": c.vocab + 1, "audio_token_id": c.vocab + 2,
+            "video_token_id": c.vocab + 3, "text_config": text}
+
+
+def write_package(directory, c, named, layer_kinds, shared=0):
+    """config.json + model.safetensors (BF16 tensors, SafeTensors layout: u64 header length,
+    JSON header, 8-byte aligned, then the data)."""
+    os.makedirs(directory, exist_ok=True)
+    with open(os.path.join(directory, "config.json"), "w") as f:
+        json.dump(config_json(c, layer_kinds, shared), f)
+    header, blobs, off = {}, [], 0
+    for name, a in named.items():
+        raw = np.ascontiguousarray(a, dtype=np.uint16).tobytes()
+        header[name] = {"dtype": "BF16", "shape": list(a.shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(os.path.join(directory, "model.safetensors"), "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for raw in blobs:
+            f.write(raw)
 
 
 class Gemma4Oracle:
