@@ -138,6 +138,113 @@ def gemma_rocm_line():
             "note": "BF16 eager policy, bit-exact with the CPU decoder restatement; sequential FP32 sums per output"}
 
 
+def run_config3(args):
+    """the 8B model under continuous batching through the executor ABI. 32 sequences with
+    prompts ~U[256, 2048] (seed 0), 512-token prefill chunks interleaved with decode rows (decode rows
+    first, then prefill chunks up to a 2048-token batch budget, as runtime/src/engine/scheduling.rs:6-83),
+    256 greedy tokens each. Reports aggregate prefill and decode tok/s over the whole run."""
+    import numpy as np
+    import ribn_amd
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_c3_{os.getpid()}.gguf")
+    ribn_amd.synth_qwen_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                             ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                             embd_type=ribn_amd.GGML_Q4_K, **CFG)
+    rng = np.random.default_rng(0)
+    n_seq, n_out, chunk, budget = 32, args.c3_tokens, 512, 2048
+    prompts = [rng.integers(0, CFG["vocab"], int(n)).tolist() for n in rng.integers(256, 2049, n_seq)]
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=2048 + n_out + 16, max_sequences=n_seq,
+                               max_batch_tokens=budget) as m:
+            seqs = {}
+            for i, p in enumerate(prompts):
+                a = m.admit(1000 + i, i + 1, p, n_out)
+                assert a.kind == ribn_amd.ADMIT_READY, a
+                seqs[i + 1] = {"prompt": p, "prefix": 0, "out": 0}
+            prefill_tokens = decode_tokens = 0
+            first_token_s = []
+            t0 = time.perf_counter()
+            while any(s["out"] < n_out for s in seqs.values()):
+                batch, used = [], 0
+                for sid, s in seqs.items():
+                    if s["out"] < n_out and s["prefix"] >= len(s["prompt"]):
+                        batch.append(ribn_amd.BatchItem(sid, ribn_amd.STEP_DECODE, s["prefix"], 1, 1))
+                        used += 1
+                for sid, s in seqs.items():
+                    left = len(s["prompt"]) - s["prefix"]
+                    if left > 0 and used < budget:
+                        n = min(chunk, left, budget - used)
+                        end = s["prefix"] + n
+                        batch.append(ribn_amd.BatchItem(sid, ribn_amd.STEP_PREFILL, s["prefix"], n,
+                                                        int(end == len(s["prompt"]))))
+                        used += n
+                m.prepare(batch)
+                sub = m.submit(batch)
+                res = None
+                while res is None:
+                    res = m.poll(sub)
+                for b, c in zip(batch, res):
+                    s = seqs[c.sequence]
+                    if b.kind == ribn_amd.STEP_PREFILL:
+                        prefill_tokens += b.token_budget
+                        if b.output_budget:
+                            first_token_s.append(time.perf_counter() - t0)
+                    else:
+                        decode_tokens += 1
+                    s["prefix"] = c.prefix
+                    s["out"] += len(c.tokens)
+            wall = time.perf_counter() - t0
+            for sid in seqs:
+                m.release(sid)
+    finally:
+        os.unlink(path)
+    out = {"metric": "configs[3] continuous batching: aggregate tok/s (8B Q4_K_M, 32 sequences)",
+           "value": round((prefill_tokens + decode_tokens) / wall, 1), "unit": "tok/s (prompt + generated)",
+           "n_gpus": 1, "higher_is_better": True, "wall_s": round(wall, 2),
+           "prompt_tokens": prefill_tokens, "generated_tokens": decode_tokens + n_seq,
+           "decode_rows_per_s": round(decode_tokens / wall, 1),
+           "median_first_token_s": round(float(np.median(first_token_s)), 2),
+           "config": {"workload": "BASELINE configs[3]", "sequences": n_seq, "prompt": "U[256,2048]",
+                      "chunk": chunk, "batch_token_budget": budget, "decode_tokens": n_out},
+           "note": "each decode row runs its own batch-1 step (matvec path); prefill rows run chunked MFMA prefill"}
+    print(json.dumps(out))
+
+
+def run_config4(args):
+    """32B-shape Q4_K_M, a 32768-token prompt prefilled in 2048-token chunks, then 256 greedy
+    tokens; split-K decode attention over the 32K cache dominates beside the 20 GB weight stream."""
+    import ribn_amd
+    cfg = dict(CFG, hidden=5120, layers=64, q_heads=64, kv_heads=8, head_dim=128, ffn=25600)
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_c4_{os.getpid()}.gguf")
+    t0 = time.time()
+    ribn_amd.synth_qwen_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                             ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                             embd_type=ribn_amd.GGML_Q4_K, **cfg)
+    t_synth = time.time() - t0
+    import numpy as np
+    prompt = np.random.default_rng(0).integers(0, cfg["vocab"], args.c4_prompt).tolist()
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=args.c4_prompt + 256 + 16, max_sequences=1,
+                               max_batch_tokens=2048) as m:
+            info = m.info
+            toks, tm = m.generate(prompt, 257)
+    finally:
+        os.unlink(path)
+    decode_tps = 256 / (tm.decode_ms / 1000.0)
+    step_bytes, _ = algorithmic_bytes_per_token(info, args.c4_prompt + 128)
+    out = {"metric": "configs[4] 32B-shape Q4_K_M at 32K context: decode tok/s; prefill tok/s",
+           "value": round(decode_tps, 2), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+           "prefill_tok_s": round(args.c4_prompt / (tm.prefill_ms / 1000.0), 1),
+           "ms_per_step": round(tm.decode_ms / 256, 3),
+           "step_hbm": {"bytes_per_token": int(step_bytes),
+                        "achieved_gbs": round(step_bytes / (tm.decode_ms / 256 / 1e3) / 1e9, 1)},
+           "config": {"workload": "BASELINE configs[4]", "prompt": args.c4_prompt, "prefill_chunk": 2048,
+                      "decode_tokens": 256, "layers": cfg["layers"]},
+           "setup_s": {"synth": round(t_synth, 1)}}
+    print(json.dumps(out))
+
+
 def probe_traffic():
     """Launch sequence measured by the FETCH_SIZE / WRITE_SIZE passes: 20 replays each of the layer-0 gate/up,
     ffn_down and head matvecs (same kernels and shapes as the 36-layer model), then 5 copies of 1 GiB between
@@ -181,6 +288,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--model", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--config", type=int, default=2,
+                    help="2: the headline line (default); 3 or 4: the configs[3] / configs[4] runs as their own line")
+    ap.add_argument("--c3-tokens", type=int, default=256)
+    ap.add_argument("--c4-prompt", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: replays the gate/up, down and head "
@@ -195,6 +306,12 @@ def main():
 
     if args.probe_traffic:
         probe_traffic()
+        return
+    if args.config == 3:
+        run_config3(args)
+        return
+    if args.config == 4:
+        run_config4(args)
         return
     cfg = dict(CFG)
     if args.layers:

@@ -933,7 +933,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(hipMemsetAsync(M->counters, 0, sizeof(uint32_t) * n_counters, M->stream));
     HIPCHK(dalloc(M, &M->head_partial, sizeof(uint64_t) * std::max<size_t>((size_t)M->V / 2 + 64, 8192)));
     {
-        M->chunk = (int)std::min<uint32_t>(M->max_batch_tokens, 512);
+        M->chunk = (int)std::min<uint32_t>(M->max_batch_tokens, 2048);
         const size_t c = (size_t)M->chunk;
         const size_t kmax = (size_t)std::max(std::max(M->H, M->F), qd);
         HIPCHK(dalloc(M, &M->p_h, sizeof(float) * c * M->H));

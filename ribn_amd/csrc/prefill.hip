@@ -26,7 +26,16 @@ constexpr int kGemmThreads = 256;
 constexpr int kTileM = 128;   // chunk rows per workgroup
 constexpr int kTileN = 128;   // weight rows per workgroup
 constexpr int kTileK = 128;   // half a Q4_K / Q6_K super-block, four Q8_0 blocks
-constexpr int kLdsRow = kTileK + 8;   // halves per LDS row (16-byte pad against bank conflicts)
+#ifndef RIBN_PG_PAD
+#define RIBN_PG_PAD 8
+#endif
+#ifndef RIBN_PG_REMAP
+#define RIBN_PG_REMAP 0
+#endif
+#ifndef RIBN_PG_DEPTH
+#define RIBN_PG_DEPTH 1
+#endif
+constexpr int kLdsRow = kTileK + RIBN_PG_PAD;   // halves per LDS row (padded against bank conflicts)
 
 __device__ __forceinline__ float h2f_bits(uint32_t b) { return __half2float(__ushort_as_half((unsigned short)(b & 0xffffu))); }
 __device__ __forceinline__ float canon(uint32_t b) {
@@ -227,46 +236,47 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     const int n_kt = (g.k + kTileK - 1) / kTileK;
     const int ks = max(1, g.ksplit), z = blockIdx.z;
     const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
-    const int wr = tid >> 1, wq = tid & 1;   // dequant: row of the tile, quarter of the K tile
+    // dequant: row of the tile, quarter of the K tile
+    const int wr = RIBN_PG_REMAP ? 32 * wave + (lane & 31) : tid >> 1, wq = RIBN_PG_REMAP ? lane >> 5 : tid & 1;
     const size_t wrow = (size_t)min(n0 + wr, n_rows - 1);
     const bool use_b = si == 2 && TB != TA;
-    // next tile in registers: X slice (128 rows x 128 halves = 2048 16-byte
-    // chunks, 8 per thread) and this thread's weight quarter
-    u4v_t xr[8];
-    QuarterRaw<TA> ra;
-    QuarterRaw<TB> rb;
-    auto fetch = [&](int kt) {
+    // K tiles in flight in registers: X slice (128 rows x 128 halves = 2048
+    // 16-byte chunks, 8 per thread) and this thread's weight quarter
+    struct Stage {
+        u4v_t xr[8];
+        QuarterRaw<TA> ra;
+        QuarterRaw<TB> rb;
+    };
+    auto fetch = [&](Stage& st, int kt) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int idx = j * kGemmThreads + tid;
             const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
-            xr[j] = u4v_t{0u, 0u, 0u, 0u};
-            if (m0 + r < g.m && col < g.k) xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
+            st.xr[j] = u4v_t{0u, 0u, 0u, 0u};
+            if (m0 + r < g.m && col < g.k) st.xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
         }
         if constexpr (TB != TA) {
-            if (use_b) rb.fetch(sg.w, wrow, kt, wq);
-            else ra.fetch(sg.w, wrow, kt, wq);
+            if (use_b) st.rb.fetch(sg.w, wrow, kt, wq);
+            else st.ra.fetch(sg.w, wrow, kt, wq);
         } else {
-            ra.fetch(sg.w, wrow, kt, wq);
+            st.ra.fetch(sg.w, wrow, kt, wq);
         }
     };
-    if (kt0 < kt1) fetch(kt0);
-    for (int kt = kt0; kt < kt1; kt++) {
-        __syncthreads();   // the previous tile's MFMA reads are done
+    auto stage = [&](const Stage& st) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int idx = j * kGemmThreads + tid;
-            *reinterpret_cast<u4v_t*>(xs + (idx >> 4) * kLdsRow + (idx & 15) * 8) = xr[j];
+            *reinterpret_cast<u4v_t*>(xs + (idx >> 4) * kLdsRow + (idx & 15) * 8) = st.xr[j];
         }
         if constexpr (TB != TA) {
-            if (use_b) rb.convert(ws + wr * kLdsRow + 64 * wq);
-            else ra.convert(ws + wr * kLdsRow + 64 * wq);
+            if (use_b) st.rb.convert(ws + wr * kLdsRow + 64 * wq);
+            else st.ra.convert(ws + wr * kLdsRow + 64 * wq);
         } else {
-            ra.convert(ws + wr * kLdsRow + 64 * wq);
+            st.ra.convert(ws + wr * kLdsRow + 64 * wq);
         }
-        __syncthreads();
-        if (kt + 1 < kt1) fetch(kt + 1);
+    };
+    auto multiply = [&]() {
 #pragma unroll
         for (int ks = 0; ks < kTileK / 32; ks++) {
             const int kk = ks * 32 + 8 * (lane >> 4);
@@ -281,7 +291,36 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
                 acc[mb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[1], acc[mb][1], 0, 0, 0);
             }
         }
+    };
+#if RIBN_PG_DEPTH == 2
+    // two tiles ahead: the loads of tile kt + 2 are issued while tile kt is multiplied
+    Stage s0, s1;
+    if (kt0 < kt1) fetch(s0, kt0);
+    if (kt0 + 1 < kt1) fetch(s1, kt0 + 1);
+    for (int kt = kt0; kt < kt1; kt += 2) {
+        __syncthreads();   // the previous tile's MFMA reads are done
+        stage(s0);
+        __syncthreads();
+        if (kt + 2 < kt1) fetch(s0, kt + 2);
+        multiply();
+        if (kt + 1 >= kt1) break;
+        __syncthreads();
+        stage(s1);
+        __syncthreads();
+        if (kt + 3 < kt1) fetch(s1, kt + 3);
+        multiply();
     }
+#else
+    Stage s0;
+    if (kt0 < kt1) fetch(s0, kt0);
+    for (int kt = kt0; kt < kt1; kt++) {
+        __syncthreads();   // the previous tile's MFMA reads are done
+        stage(s0);
+        __syncthreads();
+        if (kt + 1 < kt1) fetch(s0, kt + 1);
+        multiply();
+    }
+#endif
     // epilogue: C[m][n] of block (mb, nb): m = 16 mb + 4 (lane / 16) + i, n = 16 nb + lane % 16
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
