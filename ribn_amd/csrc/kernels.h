@@ -221,6 +221,37 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);
 int matvec_rows_per_wg(const MvArgs& a);
 size_t matvec_lds_bytes(int k);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+
+// Batched decode: one decode row per sequence, all in one step. Row r consumes
+// the token at position pos[r] of the sequence in slot slot[r]; its page table
+// is pages + slot[r] * max_pages.
+struct DecodeRows {
+    int rows;
+    const int32_t* slot;
+    const int32_t* pos;
+    const int32_t* pages;      // [slots][max_pages]
+    int max_pages;
+    const float* raw;          // [rows][ld_raw] q | k | v projections
+    int ld_raw;
+    float* out;                // [rows][ld_out] attention output
+    int ld_out;
+    float* rope;               // [rows][rot] cos | sin of each row's position
+    float* part;               // [rows][part_stride] split partials
+    size_t part_stride;
+    uint32_t* counters;        // [rows][hkv] (left at 0)
+};
+// decode attention (split-K over each row's own cache; base carries the layer's
+// weights, caches and n_splits); grid splits x hkv x rows
+hipError_t launch_attention_rows(const AttnArgs& base, const DecodeRows& r, hipStream_t stream);
+// rope[r] = cos | sin of pos[r] * inv_freq
+hipError_t launch_rope_rows(const float* inv_freq, int rot, const DecodeRows& r, hipStream_t stream);
+// token of each row: tokens[slot[r] * ld + pos[r]]
+hipError_t launch_gather_row_tokens(const uint32_t* tokens, int ld, const DecodeRows& r, uint32_t* out,
+                                    hipStream_t stream);
+// greedy argmax of each row of logits [rows][V] (first maximum, NaN skipped), written as the
+// next token of the row's sequence: tokens[pos + 1], last_token, and pos advanced by one
+hipError_t launch_rows_argmax_commit(const float* logits, int V, const DecodeRows& r, SeqState* slots,
+                                     hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t stream);
 hipError_t launch_dequant(const QMat& w, float* out, hipStream_t stream);

@@ -118,6 +118,84 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* logits, u
 }
 
 template <int HD, int G, bool F16>
+__global__ __launch_bounds__(kThreads) void attention_rows_kernel(AttnArgs a, DecodeRows r) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int row = blockIdx.z;
+    AttnArgs ar = a;
+    ar.raw = r.raw + (size_t)row * r.ld_raw;
+    ar.out = r.out + (size_t)row * r.ld_out;
+    ar.rope = r.rope + (size_t)row * a.rot;
+    ar.part = r.part + (size_t)row * r.part_stride;
+    ar.counters = r.counters + (size_t)row * a.hkv;
+    attention_item<HD, G, F16, false>(ar, blockIdx.x, blockIdx.y, r.pos[row], r.pages + (size_t)r.slot[row] * r.max_pages,
+                                      lds, NoSync{});
+}
+
+__global__ __launch_bounds__(kThreads) void rope_rows_kernel(const float* inv_freq, int half, DecodeRows r) {
+    const int row = blockIdx.x;
+    const float pos = (float)r.pos[row];
+    for (int p = threadIdx.x; p < half; p += kThreads) {
+        const float theta = pos * inv_freq[p];
+        r.rope[(size_t)row * 2 * half + p] = cosf(theta);
+        r.rope[(size_t)row * 2 * half + half + p] = sinf(theta);
+    }
+}
+
+__global__ void gather_row_tokens_kernel(const uint32_t* tokens, int ld, DecodeRows r, uint32_t* out) {
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    if (row < r.rows) out[row] = tokens[(size_t)r.slot[row] * ld + r.pos[row]];
+}
+
+__global__ __launch_bounds__(1024) void rows_argmax_commit_kernel(const float* logits, int V, DecodeRows r,
+                                                                  SeqState* slots) {
+    __shared__ uint64_t wbest[16];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* lg = logits + (size_t)row * V;
+    uint64_t b = 0ull;
+    for (int i = tid; i < V; i += 1024) b = max(b, argmax_key(lg[i], (uint32_t)i));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
+    if (lane == 0) wbest[wave] = b;
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < 16; i++) wbest[0] = max(wbest[0], wbest[i]);
+        const uint32_t tok = wbest[0] ? 0xffffffffu - (uint32_t)(wbest[0] & 0xffffffffu) : 0u;
+        SeqState* s = &slots[r.slot[row]];
+        const int pos = r.pos[row];
+        if (pos + 1 <= s->max_ctx) s->tokens[pos + 1] = tok;
+        s->last_token = tok;
+        s->pos = pos + 1;
+    }
+}
+
+template <int HD, int G, bool F16>
+hipError_t attention_rows_launch(const AttnArgs& a, const DecodeRows& r, hipStream_t st) {
+    constexpr size_t lds = sizeof(AttnLds<HD, G>);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_rows_kernel<HD, G, F16>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    attention_rows_kernel<HD, G, F16><<<dim3(a.n_splits, a.hkv, r.rows), kThreads, lds, st>>>(a, r);
+    return hipGetLastError();
+}
+
+template <int HD, bool F16>
+hipError_t attention_rows_dispatch(const AttnArgs& a, const DecodeRows& r, hipStream_t st) {
+    switch (a.hq / a.hkv) {
+    case 1: return attention_rows_launch<HD, 1, F16>(a, r, st);
+    case 2: return attention_rows_launch<HD, 2, F16>(a, r, st);
+    case 3: return attention_rows_launch<HD, 3, F16>(a, r, st);
+    case 4: return attention_rows_launch<HD, 4, F16>(a, r, st);
+    case 5: return attention_rows_launch<HD, 5, F16>(a, r, st);
+    case 6: return attention_rows_launch<HD, 6, F16>(a, r, st);
+    case 7: return attention_rows_launch<HD, 7, F16>(a, r, st);
+    case 8: return attention_rows_launch<HD, 8, F16>(a, r, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int HD, int G, bool F16>
 hipError_t attention_launch(const AttnArgs& a, hipStream_t st) {
     constexpr size_t lds = sizeof(AttnLds<HD, G>);
     if (lds > 65536) {
@@ -191,6 +269,32 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
     if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_rows(const AttnArgs& a, const DecodeRows& r, hipStream_t st) {
+    if (r.rows < 1 || a.n_splits < 1 || a.n_splits > kMaxSplits || a.hkv < 1 || a.hq % a.hkv || a.rot > a.hd ||
+        a.rot % 2)
+        return hipErrorInvalidValue;
+    if (a.hd == 128) return a.kv_f16 ? attention_rows_dispatch<128, true>(a, r, st) : attention_rows_dispatch<128, false>(a, r, st);
+    if (a.hd == 64) return a.kv_f16 ? attention_rows_dispatch<64, true>(a, r, st) : attention_rows_dispatch<64, false>(a, r, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_rope_rows(const float* inv_freq, int rot, const DecodeRows& r, hipStream_t st) {
+    rope_rows_kernel<<<r.rows, kThreads, 0, st>>>(inv_freq, rot / 2, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_row_tokens(const uint32_t* tokens, int ld, const DecodeRows& r, uint32_t* out,
+                                    hipStream_t st) {
+    gather_row_tokens_kernel<<<(r.rows + 63) / 64, 64, 0, st>>>(tokens, ld, r, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rows_argmax_commit(const float* logits, int V, const DecodeRows& r, SeqState* slots,
+                                     hipStream_t st) {
+    rows_argmax_commit_kernel<<<r.rows, 1024, 0, st>>>(logits, V, r, slots);
+    return hipGetLastError();
 }
 
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t st) {

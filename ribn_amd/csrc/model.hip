@@ -106,6 +106,14 @@ struct ribn_rocm_model {
     // chunked prefill buffers (prefill.hip), rows per chunk = chunk
     int chunk = 0;
     float *p_h = nullptr, *p_qkv = nullptr, *p_q = nullptr, *p_gu = nullptr, *p_part = nullptr;
+    // batched decode (one row per sequence through the prefill GEMMs): rows <= max_rows
+    int b_rows = 0;
+    int32_t* d_brows = nullptr;            // [2][b_rows]: slot, pos
+    std::vector<int32_t> h_brows;
+    uint32_t* d_btokens = nullptr;
+    float *b_att = nullptr, *b_rope = nullptr, *b_part = nullptr, *b_logits = nullptr;
+    size_t b_part_stride = 0;
+    uint32_t* b_counters = nullptr;
     size_t p_part_floats = 0;
     uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
 
@@ -662,6 +670,80 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     return e;
 }
 
+// One decode row per sequence, all in one step (batched decode): row r
+// consumes the token at position pos[r] of the sequence in slot[r] and samples
+// the next one. The projections run as the chunked-prefill MFMA GEMMs over the
+// rows; attention is the split-K decode kernel over each row's own cache; the
+// head is one GEMM over the rows followed by a per-row argmax.
+hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const std::vector<int>& pos) {
+    hipStream_t st = M->stream;
+    const int n = (int)slots.size();
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd, ldq = qd + 2 * kd;
+    int max_ctx = 0;
+    for (int r = 0; r < n; r++) {
+        M->h_brows[r] = slots[r];
+        M->h_brows[n + r] = pos[r];
+        max_ctx = std::max(max_ctx, pos[r] + 1);
+    }
+    hipError_t e = hipMemcpyAsync(M->d_brows, M->h_brows.data(), sizeof(int32_t) * 2 * n, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return e;
+    DecodeRows dr{};
+    dr.rows = n;
+    dr.slot = M->d_brows;
+    dr.pos = M->d_brows + n;
+    dr.pages = M->d_pages;
+    dr.max_pages = M->max_pages;
+    dr.raw = M->p_qkv;
+    dr.ld_raw = ldq;
+    dr.out = M->b_att;
+    dr.ld_out = qd;
+    dr.rope = M->b_rope;
+    dr.part = M->b_part;
+    dr.part_stride = M->b_part_stride;
+    dr.counters = M->b_counters;
+    if ((e = launch_gather_row_tokens(M->d_tokens, M->context + 1, dr, M->d_btokens, st)) != hipSuccess) return e;
+    if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
+    if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
+    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs) {
+        PrefillGemm g{};
+        g.x = x; g.m = n; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
+        int tiles = 0;
+        for (const PrefillSeg& sg : segs) {
+            g.seg[g.nseg] = sg;
+            g.seg[g.nseg].tile0 = tiles;
+            tiles += (int)((sg.w.rows + 127) / 128);
+            g.nseg++;
+        }
+        g.ksplit = prefill_gemm_splits(n, k, tiles);
+        if (g.ksplit > 1 && (size_t)g.ksplit * n * ldy <= M->p_part_floats) g.part = M->p_part;
+        else g.ksplit = 1;
+        return launch_prefill_gemm(g, st);
+    };
+    const int n_splits = splits_for_ctx(max_ctx);
+    for (int l = 0; l < M->L; l++) {
+        const Layer& y = M->layers[l];
+        if ((e = launch_rows_rms_f16(M->p_h, n, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
+                      {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
+                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
+            return e;
+        AttnArgs at = attn_args(M, l, n_splits);
+        if ((e = launch_attention_rows(at, dr, st)) != hipSuccess) return e;
+        if ((e = launch_rows_rms_f16(M->b_att, n, qd, nullptr, 0.f, false, M->p_att16, qd, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}})) != hipSuccess) return e;
+        if ((e = launch_rows_rms_f16(M->p_h, n, M->H, y.ffn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
+                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}})) != hipSuccess)
+            return e;
+        if ((e = launch_silu_mul_f16(M->p_gu, M->F, n, M->p_act16, st)) != hipSuccess) return e;
+        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}})) != hipSuccess) return e;
+    }
+    if ((e = launch_rows_rms_f16(M->p_h, n, M->H, M->out_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+    if ((e = gemm(M->p_x16, M->H, M->b_logits, M->V, MV_STORE, {PrefillSeg{M->out, 0, 0, nullptr}})) != hipSuccess)
+        return e;
+    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);
+}
+
 // Prompt rows pos0 .. pos0 + n - 1 of the sequence in `slot` in chunks of at
 // most M->chunk rows; the last chunk samples the next token when `final`.
 hipError_t prefill_rows(ribn_rocm_model* M, int slot, int pos0, int n, bool final) {
@@ -951,6 +1033,21 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
                                   std::max(need(M->H, 2 * M->F, t_gu), need(M->F, M->H, t_h)));
         M->p_part_floats = per_row * c;
         HIPCHK(dalloc(M, &M->p_part, sizeof(float) * M->p_part_floats));
+        // batched decode rows: one per sequence, at most the chunk's rows
+        M->b_rows = (int)std::min<size_t>(c, M->max_seqs);
+        if (M->b_rows >= 2) {
+            const size_t R = (size_t)M->b_rows;
+            M->b_part_stride = (size_t)M->hkv * kMaxSplits * ((size_t)(M->hq / M->hkv) * M->hd + 2 * (M->hq / M->hkv));
+            HIPCHK(dalloc(M, &M->d_brows, sizeof(int32_t) * 2 * R));
+            HIPCHK(dalloc(M, &M->d_btokens, sizeof(uint32_t) * R));
+            HIPCHK(dalloc(M, &M->b_att, sizeof(float) * R * qd));
+            HIPCHK(dalloc(M, &M->b_rope, sizeof(float) * R * M->rot));
+            HIPCHK(dalloc(M, &M->b_part, sizeof(float) * R * M->b_part_stride));
+            HIPCHK(dalloc(M, &M->b_logits, sizeof(float) * R * M->V));
+            HIPCHK(dalloc(M, &M->b_counters, sizeof(uint32_t) * R * M->hkv));
+            HIPCHK(hipMemsetAsync(M->b_counters, 0, sizeof(uint32_t) * R * M->hkv, M->stream));
+            M->h_brows.assign(2 * R, 0);
+        }
     }
 
     const int slots = (int)M->max_seqs + 1;
@@ -1233,7 +1330,32 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
     M->prepared.clear();
     hipError_t e = hipSuccess;
     if (!M->pending.done) e = hipEventCreateWithFlags(&M->pending.done, hipEventDisableTiming);
+    // decode rows (one token, sampled) of two or more sequences run as one batched step
+    std::vector<char> batched(n, 0);
+    if (M->b_rows >= 2 && M->step_wg == 0) {
+        std::vector<int> bslots, bpos;
+        std::vector<size_t> brow;
+        for (size_t r = 0; r < n; r++) {
+            const ribn_rocm_batch_item& it = items[r];
+            if (it.kind == RIBN_STEP_DECODE && it.token_budget == 1 && it.output_budget == 1 && (int)bslots.size() < M->b_rows) {
+                bslots.push_back(M->seqs[it.sequence].slot);
+                bpos.push_back((int)it.prefix);
+                brow.push_back(r);
+            }
+        }
+        if (bslots.size() >= 2) {
+            for (size_t i = 0; i < brow.size(); i++) {
+                batched[brow[i]] = 1;
+                M->seqs[items[brow[i]].sequence].in_flight = true;
+            }
+            e = decode_rows(M, bslots, bpos);
+            for (size_t i = 0; e == hipSuccess && i < brow.size(); i++)
+                e = hipMemcpyAsync(&M->h_out[brow[i]], &M->d_slots[bslots[i]].last_token, 4, hipMemcpyDeviceToHost,
+                                   M->stream);
+        }
+    }
     for (size_t r = 0; e == hipSuccess && r < n; r++) {
+        if (batched[r]) continue;
         const ribn_rocm_batch_item& it = items[r];
         Sequence& s = M->seqs[it.sequence];
         s.in_flight = true;

@@ -254,7 +254,21 @@ def _run_engine(m, prompts, max_out, chunk=5):
     return [seqs[i + 1]["out"] for i in range(len(prompts))]
 
 
+def _near_tie_match(name, got, ref, ref_logits):
+    """Greedy streams agree, or diverge only where the oracle's top-2 margin is a near tie; the
+    comparison stops at a divergence (the continuations differ from there on)."""
+    for i, (a, b) in enumerate(zip(got, ref)):
+        if a != b:
+            l = ref_logits[i]
+            margin = l[b] - l[a]
+            assert margin <= 2e-3 * abs(l[b]) + 1e-3, f"{name} step {i}: {a} vs {b}, oracle margin {margin:.3e}"
+            say(f"  {name}: near-tie at step {i} (margin {margin:.2e}); stop comparing")
+            return
+
+
 def test_executor_matches_generate(model_paths):
+    """The executor's rows (chunked prefill, then batched decode of the three sequences through the MFMA
+    GEMMs) against batch-1 generate and the oracle."""
     path = model_paths["qwen3_q4km_hd64"]
     rng = np.random.default_rng(4)
     prompts = [rng.integers(0, 512, n).tolist() for n in (7, 12, 3)]
@@ -263,8 +277,25 @@ def test_executor_matches_generate(model_paths):
         outs = _run_engine(m, prompts, 6)
         for p, o in zip(prompts, outs):
             g, _ = m.generate(p, 6)
-            assert g.tolist() == o
+            ref, ref_logits = _oracle_greedy(path, p, 6, 64, KV_MODES["f16"][0])
+            _near_tie_match("generate", g.tolist(), ref, ref_logits)
+            _near_tie_match("executor", o, ref, ref_logits)
         m.synchronize()
+
+
+@pytest.mark.parametrize("name", ["qwen3_q4km_hd128_g4", "qwen2_q8_0_g7", "qwen3_g8_tied"])
+def test_batched_decode_rows_match_oracle(model_paths, name):
+    """Five sequences decoding together: every batch's decode rows run as one batched step (per-row
+    positions and page tables, split-K attention per row, GEMM head, per-row argmax)."""
+    path = model_paths[name]
+    rng = np.random.default_rng(6)
+    prompts = [rng.integers(0, MODELS[name]["vocab"], n).tolist() for n in (5, 17, 9, 33, 2)]
+    say(f"batched decode {name}")
+    with ribn_amd.QwenRocm(path, context_tokens=64, max_sequences=5, max_batch_tokens=64) as m:
+        outs = _run_engine(m, prompts, 12)
+    for p, o in zip(prompts, outs):
+        ref, ref_logits = _oracle_greedy(path, p, 12, 64, KV_MODES["f16"][0])
+        _near_tie_match(name, o, ref, ref_logits)
 
 
 def test_executor_contract_errors(model_paths):
