@@ -239,7 +239,15 @@ struct DecodeRows {
     float* part;               // [rows][part_stride] split partials
     size_t part_stride;
     uint32_t* counters;        // [rows][hkv] (left at 0)
+    int split_tokens;          // positions per split: a row splits its context into
+                               // rows_splits(ctx, split_tokens) parts
 };
+// power of two >= ctx / split_tokens, at most kMaxSplits
+__host__ __device__ inline int rows_splits(int ctx, int split_tokens) {
+    int s = 1;
+    while (s * split_tokens < ctx && s < kMaxSplits) s <<= 1;
+    return s;
+}
 // decode attention (split-K over each row's own cache; base carries the layer's
 // weights, caches and n_splits); grid splits x hkv x rows
 hipError_t launch_attention_rows(const AttnArgs& base, const DecodeRows& r, hipStream_t stream);

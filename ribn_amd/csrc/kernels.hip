@@ -121,7 +121,10 @@ template <int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_rows_kernel(AttnArgs a, DecodeRows r) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int row = blockIdx.z;
+    const int ns = rows_splits(r.pos[row] + 1, r.split_tokens);
+    if ((int)blockIdx.x >= ns) return;   // a shorter row uses fewer splits
     AttnArgs ar = a;
+    ar.n_splits = ns;
     ar.raw = r.raw + (size_t)row * r.ld_raw;
     ar.out = r.out + (size_t)row * r.ld_out;
     ar.rope = r.rope + (size_t)row * a.rot;

@@ -701,6 +701,9 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     dr.part = M->b_part;
     dr.part_stride = M->b_part_stride;
     dr.counters = M->b_counters;
+    // splits per row: the rows already spread the work over the GPU, so a split
+    // covers up to 256 positions (the batch-1 step splits down to 64)
+    dr.split_tokens = 256;
     if ((e = launch_gather_row_tokens(M->d_tokens, M->context + 1, dr, M->d_btokens, st)) != hipSuccess) return e;
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
@@ -719,7 +722,7 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
         else g.ksplit = 1;
         return launch_prefill_gemm(g, st);
     };
-    const int n_splits = splits_for_ctx(max_ctx);
+    const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
         if ((e = launch_rows_rms_f16(M->p_h, n, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;

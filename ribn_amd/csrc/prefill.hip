@@ -215,21 +215,25 @@ struct QuarterRaw<8> {
 // per CU, so one stages while the other multiplies).
 // MFMA 16x16x32 f16 operand layout (lane l): A[m = l%16][k = 8(l/16) .. +8],
 // B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
-template <int TA, int TB>
+// MT (128 or 32) is the workgroup's chunk rows: 32 for batched decode rows,
+// where a 128-row tile would mostly multiply padding.
+template <int TA, int TB, int MT>
 __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
+    constexpr int MB = MT / 16;                // 16-row MFMA blocks
+    constexpr int XR = MT * 16 / kGemmThreads; // X chunks per thread per K tile
     extern __shared__ __attribute__((aligned(16))) uint16_t plds[];
-    uint16_t* xs = plds;                       // [kTileM][kLdsRow]
-    uint16_t* ws = plds + kTileM * kLdsRow;    // [kTileN][kLdsRow]
+    uint16_t* xs = plds;                       // [MT][kLdsRow]
+    uint16_t* ws = plds + MT * kLdsRow;        // [kTileN][kLdsRow]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int si = 0;
     if (g.nseg > 1 && (int)blockIdx.x >= g.seg[1].tile0) si = 1;
     if (g.nseg > 2 && (int)blockIdx.x >= g.seg[2].tile0) si = 2;
     const PrefillSeg sg = g.seg[si];
-    const int m0 = blockIdx.y * kTileM, n0 = ((int)blockIdx.x - sg.tile0) * kTileN;
+    const int m0 = blockIdx.y * MT, n0 = ((int)blockIdx.x - sg.tile0) * kTileN;
     const int n_rows = (int)sg.w.rows;
-    f4_t acc[8][2];
+    f4_t acc[MB][2];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < MB; i++) {
         acc[i][0] = f4_t{0.f, 0.f, 0.f, 0.f};
         acc[i][1] = f4_t{0.f, 0.f, 0.f, 0.f};
     }
@@ -243,13 +247,13 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     // K tiles in flight in registers: X slice (128 rows x 128 halves = 2048
     // 16-byte chunks, 8 per thread) and this thread's weight quarter
     struct Stage {
-        u4v_t xr[8];
+        u4v_t xr[XR];
         QuarterRaw<TA> ra;
         QuarterRaw<TB> rb;
     };
     auto fetch = [&](Stage& st, int kt) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < XR; j++) {
             const int idx = j * kGemmThreads + tid;
             const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     };
     auto stage = [&](const Stage& st) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
+        for (int j = 0; j < XR; j++) {
             const int idx = j * kGemmThreads + tid;
             *reinterpret_cast<u4v_t*>(xs + (idx >> 4) * kLdsRow + (idx & 15) * 8) = st.xr[j];
         }
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
             for (int nb = 0; nb < 2; nb++)
                 b[nb] = *reinterpret_cast<const h8_t*>(ws + (32 * wave + 16 * nb + (lane & 15)) * kLdsRow + kk);
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++) {
+            for (int mb = 0; mb < MB; mb++) {
                 const h8_t a = *reinterpret_cast<const h8_t*>(xs + (16 * mb + (lane & 15)) * kLdsRow + kk);
                 acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[0], acc[mb][0], 0, 0, 0);
                 acc[mb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[1], acc[mb][1], 0, 0, 0);
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
         if (n >= n_rows) continue;
         const float bias = sg.bias && z == 0 ? sg.bias[n] : 0.f;
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) {
+        for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + 16 * mb + 4 * (lane >> 4) + i;
@@ -700,9 +704,12 @@ hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
 
 }  // namespace
 
+int gemm_rows_tile(int m) { return m <= 32 ? 32 : kTileM; }
+
 int prefill_gemm_splits(int m, int k, int n_tiles) {
     // enough workgroups for two per CU on 256 CUs, at least 4 K tiles per split, at most 8 splits
-    const int wgs = n_tiles * ((m + kTileM - 1) / kTileM);
+    const int mt = gemm_rows_tile(m);
+    const int wgs = n_tiles * ((m + mt - 1) / mt);
     const int n_kt = (k + kTileK - 1) / kTileK;
     int ks = 1;
     while (ks < 8 && wgs * ks < 512 && n_kt / (2 * ks) >= 4) ks *= 2;
@@ -725,16 +732,25 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
     const int ks = g.part ? max(1, g.ksplit) : 1;
     if (ks > 1 && ks > (g.k + kTileK - 1) / kTileK) return hipErrorInvalidValue;
-    const dim3 grid(tiles, (g.m + kTileM - 1) / kTileM, ks);
+    const int mt = gemm_rows_tile(g.m);
+    const dim3 grid(tiles, (g.m + mt - 1) / mt, ks);
     PrefillGemm gg = g;
     gg.ksplit = ks;
-    const size_t lds = prefill_gemm_lds_bytes();
+    const size_t lds = (size_t)(mt + kTileN) * kLdsRow * 2;
 #define RIBN_PG(A, B)                                                                                           \
     if (ta == A && tb == B) {                                                                                   \
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B>),           \
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);               \
-        if (e != hipSuccess) return e;                                                                          \
-        prefill_gemm_kernel<A, B><<<grid, kGemmThreads, lds, st>>>(gg);                                         \
+        hipError_t e;                                                                                           \
+        if (mt == 32) {                                                                                         \
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, 32>),              \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
+            if (e != hipSuccess) return e;                                                                      \
+            prefill_gemm_kernel<A, B, 32><<<grid, kGemmThreads, lds, st>>>(gg);                                 \
+        } else {                                                                                                \
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, kTileM>),          \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
+            if (e != hipSuccess) return e;                                                                      \
+            prefill_gemm_kernel<A, B, kTileM><<<grid, kGemmThreads, lds, st>>>(gg);                             \
+        }                                                                                                       \
         e = hipGetLastError();                                                                                  \
         if (e != hipSuccess || ks == 1) return e;                                                               \
         const size_t n = (size_t)g.m * g.ldy;                                                                   \
