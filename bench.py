@@ -36,12 +36,14 @@ CFG = dict(qwen3=True, hidden=4096, layers=36, q_heads=32, kv_heads=8, head_dim=
            rope_base=1e6, rms_eps=1e-6, weight_std=0.02, seed=0)
 
 
-def algorithmic_bytes_per_token(info, ctx_mean):
-    """Encoded weight bytes streamed per token + one embedding row + norms + BF16 KV read/write."""
+def algorithmic_bytes_per_token(info, ctx_mean, embd_row=None):
+    """Encoded weight bytes streamed per token + one embedding row + norms + 16-bit KV read/write.
+    embd_row: encoded bytes of one token_embd row (default Q4_K)."""
     H, L, hkv, hd, V = info.hidden, info.layers, info.kv_heads, info.head_dim, info.vocab
-    embd_row = H // 256 * 144
+    if embd_row is None:
+        embd_row = H // 256 * 144
     norms = (2 * L + 1) * H * 4 + 2 * L * hd * 4
-    weights = info.weight_bytes - V * (H // 256) * 144 + embd_row   # token_embd is gathered, not streamed
+    weights = info.weight_bytes - V * embd_row + embd_row   # token_embd is gathered, not streamed
     kv = ctx_mean * 2 * L * hkv * hd * 2 + 2 * L * hkv * hd * 2
     return weights + norms + kv, weights
 
@@ -218,6 +220,37 @@ def run_config3(args):
     print(json.dumps(out))
 
 
+def run_config1(args):
+    """Qwen2.5-0.5B shape, every matrix Q8_0 (embedding and output too), q/k/v bias, a
+    128-token random prompt, then 256 greedy tokens at batch 1."""
+    import ribn_amd
+    cfg = dict(qwen3=False, hidden=896, layers=24, q_heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936,
+               rope_base=1e6, rms_eps=1e-6, weight_std=0.02, seed=0)
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_c1_{os.getpid()}.gguf")
+    q8 = ribn_amd.GGML_Q8_0
+    ribn_amd.synth_qwen_gguf(path, weight_type=q8, attn_v_type=q8, ffn_down_type=q8, output_type=q8, embd_type=q8,
+                             **cfg)
+    import numpy as np
+    prompt = np.random.default_rng(0).integers(0, cfg["vocab"], 128).tolist()
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=128 + 256 + 16, max_sequences=1) as m:
+            info = m.info
+            m.generate(prompt, 16)
+            toks, tm = m.generate(prompt, 257)
+    finally:
+        os.unlink(path)
+    decode_tps = 256 / (tm.decode_ms / 1000.0)
+    step_bytes, _ = algorithmic_bytes_per_token(info, 128 + 128, embd_row=cfg["hidden"] // 32 * 34)
+    out = {"metric": "configs[1] Qwen2.5-0.5B-shape Q8_0 bs1: decode tok/s; prefill tok/s",
+           "value": round(decode_tps, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+           "prefill_tok_s": round(128 / (tm.prefill_ms / 1000.0), 1), "ms_per_step": round(tm.decode_ms / 256, 4),
+           "step_hbm": {"bytes_per_token": int(step_bytes),
+                        "achieved_gbs": round(step_bytes / (tm.decode_ms / 256 / 1e3) / 1e9, 1)},
+           "config": {"workload": "BASELINE configs[1]", "prompt": 128, "decode_tokens": 256, "layers": 24}}
+    print(json.dumps(out))
+
+
 def run_config4(args):
     """32B-shape Q4_K_M, a 32768-token prompt prefilled in 2048-token chunks, then 256 greedy
     tokens; split-K decode attention over the 32K cache dominates beside the 20 GB weight stream."""
@@ -297,7 +330,7 @@ def main():
     ap.add_argument("--model", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--config", type=int, default=2,
-                    help="2: the headline line (default); 3 or 4: the configs[3] / configs[4] runs as their own line")
+                    help="2: the headline line (default); 1, 3 or 4: the configs[1] / [3] / [4] runs as their own line")
     ap.add_argument("--c3-tokens", type=int, default=256)
     ap.add_argument("--c4-prompt", type=int, default=32768)
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
@@ -314,6 +347,9 @@ def main():
 
     if args.probe_traffic:
         probe_traffic()
+        return
+    if args.config == 1:
+        run_config1(args)
         return
     if args.config == 3:
         run_config3(args)
