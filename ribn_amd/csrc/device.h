@@ -763,7 +763,7 @@ struct AttnLds {
     static constexpr int NS = kThreads / (HD / 8);
     float buf[G + 2][HD];                // q heads, k, v of the current token
     float rp[HD];                        // rope cos | sin
-    uint16_t kt[kTile][HD];
+    uint16_t kq[HD];                     // the current token's k at cache precision
     uint16_t vt[kTile][HD];
     float sc[G][kMaxSplitTokens];        // scores, then probabilities
     float red[kWaves][G * HD];           // P.V: one partial per wave
@@ -783,10 +783,8 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     constexpr int CH = HD / 8;                 // 16-byte chunks per row
     constexpr int NS = kThreads / CH;          // token slices in P.V
     constexpr int REC = G * HD + 2 * G;        // partial record floats
-    constexpr int DQ = HD / 4;                 // dims per lane in the scores
     AttnLds<HD, G>& L = *reinterpret_cast<AttnLds<HD, G>*>(lds_raw);
     auto& buf = L.buf;
-    auto& kt = L.kt;
     auto& vt = L.vt;
     auto& sc = L.sc;
     auto& red = L.red;
@@ -855,8 +853,26 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     for (int i = tid; i < n; i += kThreads)
         if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = pages[(t0 + i) / kPageTokens];
     __syncthreads();
-    KvTile<HD, F16> kpre, vpre;   // first tile in flight during the prologue
-    kpre.load(a.kcache, pg, a.hkv, kvh, 0, n, t0);
+    // Scores run on MFMA straight from registers: a wave takes 16-position
+    // blocks; lane (bn, bj) holds position bn's dims bj*HD/4 .. +HD/4 (KC
+    // 16-byte chunks). Its first block and the first V tile are in flight
+    // during the prologue.
+    constexpr int KC = HD / 32;
+    const int bn = lane & 15, bj = lane >> 4;
+    auto kload = [&](int blk, u4_t (&r)[KC]) {
+        const int tl = blk * 16 + bn;
+        if (tl < n) {
+            const uint16_t* src = a.kcache + ((size_t)(pg[blk] * a.hkv + kvh) * kPageTokens + (tl & 15)) * HD + bj * (HD / 4);
+#pragma unroll
+            for (int c = 0; c < KC; c++) r[c] = *reinterpret_cast<const u4_t*>(src + 8 * c);
+        } else {
+#pragma unroll
+            for (int c = 0; c < KC; c++) r[c] = u4_t{0u, 0u, 0u, 0u};
+        }
+    };
+    u4_t kc[KC];
+    kload(wave, kc);
+    KvTile<HD, F16> vpre;
     vpre.load(a.vcache, pg, a.hkv, kvh, 0, n, t0);
     sync.phase(1);
     if (!sync()) return false;
@@ -935,6 +951,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         }
         for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
     }
+    if (hold_k) *reinterpret_cast<uint2*>(&L.kq[4 * pc]) = cur_k;
     if (owner && (hold_k || hold_v)) {
         const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
         uint16_t* dst = (hold_k ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
@@ -943,48 +960,55 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     __syncthreads();
 
     sync.phase(3);
-    // -- scores, tile by tile: lane group of 4 per position
-    const int stl = tid >> 2, part = tid & 3;
-    for (int c0 = 0; c0 < n; c0 += kTile) {
-        if (c0 == 0) kpre.store(kt);
-        else {
-            KvTile<HD, F16> kk;
-            kk.load(a.kcache, pg, a.hkv, kvh, c0, n, t0);
-            kk.store(kt);
-        }
-        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
-            __syncthreads();
-            if (hold_k) *reinterpret_cast<uint2*>(&kt[pos - t0 - c0][4 * pc]) = cur_k;
-        }
-        __syncthreads();
-        const int tl = c0 + stl;
-        float acc[G];
+    // -- scores S[head][position] = Q K^T (v_mfma_f32_16x16x32_f16). A = q
+    //    rows (heads; zero beyond G) in binary16 with log2(e)/sqrt(hd) folded
+    //    in, B = K^T from the lane's chunks; step c pairs lane group bj's
+    //    logical k 0..7 with dims bj*HD/4 + 8c .. +8 for both operands. A
+    //    bfloat16 cache is converted to binary16 (exact in binary16's normal
+    //    range). The current position's k comes from LDS, not the cache.
+    {
+        typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
+        typedef float f4v_t __attribute__((ext_vector_type(4)));
+        h8v_t qa[KC];
 #pragma unroll
-        for (int g = 0; g < G; g++) acc[g] = 0.f;
+        for (int c = 0; c < KC; c++) {
+            const int d = bj * (HD / 4) + 8 * c;
+            float4 lo{0.f, 0.f, 0.f, 0.f}, hi{0.f, 0.f, 0.f, 0.f};
+            if (bn < G) {
+                lo = *reinterpret_cast<const float4*>(&buf[bn][d]);
+                hi = *reinterpret_cast<const float4*>(&buf[bn][d + 4]);
+            }
+            qa[c] = h8v_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                          (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+        }
+        auto to_f16x2 = [](uint32_t w) -> uint32_t {
+            if constexpr (F16) return w;
+            const _Float16 x = (_Float16)__uint_as_float(w << 16), y = (_Float16)__uint_as_float(w & 0xffff0000u);
+            return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        };
+        const int nblk = (n + 15) / 16;
+        const int own_blk = owner ? (pos - t0) / 16 : -1, own_bn = (pos - t0) & 15;
+        for (int blk = wave; blk < nblk; blk += kWaves) {   // wave-uniform
+            u4_t kn[KC];
+            kload(blk + kWaves, kn);
+            if (blk == own_blk && bn == own_bn) {
 #pragma unroll
-        for (int c = 0; c < DQ / 8; c++) {
-            const int d0 = part * DQ + c * 8;
-            const u4_t kw = *reinterpret_cast<const u4_t*>(&kt[stl][d0]);
+                for (int c = 0; c < KC; c++) kc[c] = *reinterpret_cast<const u4_t*>(&L.kq[bj * (HD / 4) + 8 * c]);
+            }
+            f4v_t sacc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < KC; c++) {
+                const u4_t kb{to_f16x2(kc[c].x), to_f16x2(kc[c].y), to_f16x2(kc[c].z), to_f16x2(kc[c].w)};
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], __builtin_bit_cast(h8v_t, kb), sacc, 0, 0, 0);
+            }
+            const int tl = blk * 16 + bn;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t w = dword_at(kw, i);
-                const float k0 = kv_decode<F16>(w & 0xffffu), k1 = kv_decode<F16>(w >> 16);
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float2 qq = *reinterpret_cast<const float2*>(&buf[g][d0 + 2 * i]);
-                    acc[g] = fmaf(qq.x, k0, acc[g]);
-                    acc[g] = fmaf(qq.y, k1, acc[g]);
-                }
+                const int g = 4 * bj + i;
+                if (g < G && tl < n) sc[g][tl] = sacc[i];
             }
-        }
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            acc[g] += dpp_f<0xB1>(acc[g]);
-            acc[g] += dpp_f<0x4E>(acc[g]);
-        }
-        if (part == 0 && tl < n) {
-#pragma unroll
-            for (int g = 0; g < G; g++) sc[g][tl] = acc[g];
+            for (int c = 0; c < KC; c++) kc[c] = kn[c];
         }
         __syncthreads();
     }
@@ -1014,14 +1038,13 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < 8; i++) o[g][i] = 0.f;
+    KvTile<HD, F16> vcur = vpre;
     for (int c0 = 0; c0 < n; c0 += kTile) {
+        KvTile<HD, F16> vnext;
+        vnext.load(a.vcache, pg, a.hkv, kvh, c0 + kTile, n, t0);
         if (c0 > 0) __syncthreads();
-        if (c0 == 0) vpre.store(vt);
-        else {
-            KvTile<HD, F16> vv;
-            vv.load(a.vcache, pg, a.hkv, kvh, c0, n, t0);
-            vv.store(vt);
-        }
+        vcur.store(vt);
+        vcur = vnext;
         if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
             __syncthreads();
             if (hold_v) *reinterpret_cast<uint2*>(&vt[pos - t0 - c0][4 * pc]) = cur_v;

@@ -1618,7 +1618,10 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
     case 6: {
         // decode attention of layer 0 for a scratch sequence holding exactly
         // `ctx` positions (the current token is position ctx-1)
-        const int ctx = (int)*bytes;
+        const int ctx = (int)(*bytes & 0xffffffffu), force = (int)(*bytes >> 32);
+        if (force && (force > kMaxSplits || (force & (force - 1)) ||
+                      (ctx + force - 1) / force > kMaxSplitTokens - kPageTokens))
+            return fail(nullptr, err, err_len, "attention bench split count unusable for this context", RIBN_ERR_INVALID);
         if (ctx < 1 || (uint32_t)ctx > M->context)
             return fail(nullptr, err, err_len, "attention bench context outside the prepared context", RIBN_ERR_INVALID);
         if (!take_pages(M, (uint32_t)ctx, &bench_pages))
@@ -1631,7 +1634,7 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
         HIPCHK(hipMemcpyAsync(&M->d_slots[slot], &M->h_state[slot], sizeof(SeqState), hipMemcpyHostToDevice, M->stream));
         HIPCHK(select_slot(M, slot));
         attn = true;
-        at = attn_args(M, 0, splits_for_ctx(ctx));
+        at = attn_args(M, 0, force ? force : splits_for_ctx(ctx));
         *bytes = 0;
         break;
     }
