@@ -718,55 +718,31 @@ __device__ __forceinline__ void head_finish(const MvArgs& a, uint64_t best, int 
 // (attn_score_gqa_paged, model_ops.rs:442-590; host equations
 // qwen_reference.rs:368-461, dense Qwen3: no gate). Workgroup (split, kv head);
 // the G = hq/hkv query heads of a KV head share every K/V load.
-//  * the split's K and V are staged in LDS in tiles of 64 positions (16-byte
-//    loads, the first tile issued before the prologue so its latency overlaps);
+//  * each wave streams its own 32-position blocks of the split (16-byte loads
+//    straight into registers, the next block issued before the current one is
+//    used, a wave's first block before the prologue so its latency overlaps);
 //  * prologue: q (G heads) and k of the current token get per-head RMSNorm
 //    (qwen_reference.rs:382-400) and NeoX rope from the step table; the
 //    workgroup whose split holds the current position appends k, v
 //    (kv_append_f16, model_ops.rs:1258);
-//  * scores: 4 lanes per position, 1/4 of head_dim each, for all G heads;
-//  * exact softmax statistics of the split, then P.V over the V tiles;
+//  * scores and P.V on MFMA with an online softmax per wave; the waves merge
+//    in LDS;
 //  * splits are merged by log-sum-exp in the last workgroup of a KV head.
 // Every key and value, including the current token's, is used at the cache's
-// precision, as the reference reads its F16 cache.
-constexpr int kTile = 64;
-
-template <int HD, bool F16>
-struct KvTile {
-    static constexpr int kLoads = kTile * HD * 2 / 16 / kThreads;   // 16-byte loads per thread
-    u4_t r[kLoads];
-    // position i*kThreads/(HD/8)... : load index j -> (token, chunk)
-    __device__ __forceinline__ void load(const uint16_t* cache, const int* pg, int hkv, int kvh, int c0, int n,
-                                         int t0) {
-#pragma unroll
-        for (int j = 0; j < kLoads; j++) {
-            const int idx = j * kThreads + threadIdx.x;
-            const int tl = c0 + idx / (HD / 8), ch = idx % (HD / 8);
-            if (tl < n) {
-                const int t = t0 + tl;
-                r[j] = *reinterpret_cast<const u4_t*>(
-                    cache + ((size_t)(pg[tl / kPageTokens] * hkv + kvh) * kPageTokens + (t % kPageTokens)) * HD + ch * 8);
-            }
-        }
-    }
-    __device__ __forceinline__ void store(uint16_t (*tile)[HD]) const {
-#pragma unroll
-        for (int j = 0; j < kLoads; j++) {
-            const int idx = j * kThreads + threadIdx.x;
-            *reinterpret_cast<u4_t*>(&tile[idx / (HD / 8)][(idx % (HD / 8)) * 8]) = r[j];
-        }
-    }
-};
+// precision, as the reference reads its F16 cache; q and the probabilities
+// enter the MFMAs in binary16.
+constexpr int kVtLd = 36;   // halves per row of a wave's transposed V tile (32 positions + pad)
 
 template <int HD, int G>
 struct AttnLds {
-    static constexpr int NS = kThreads / (HD / 8);
     float buf[G + 2][HD];                // q heads, k, v of the current token
     float rp[HD];                        // rope cos | sin
-    uint16_t kq[HD];                     // the current token's k at cache precision
-    uint16_t vt[kTile][HD];
-    float sc[G][kMaxSplitTokens];        // scores, then probabilities
-    float red[kWaves][G * HD];           // P.V: one partial per wave
+    uint16_t kq[HD];                     // the current token's k and v at cache precision
+    uint16_t vq[HD];
+    uint16_t vts[kWaves][HD][kVtLd];     // per wave: V^T of its current 32-position block
+    float red[kWaves][G * HD];           // per wave: unnormalized O rows
+    float wst[kWaves][2][G];             // per wave: max, sum; then the merge weights
+    float swt[G * kMaxSplits];           // cross-split merge weights
     float stat[2][G];                    // per-head max, sum
     int pg[kMaxSplitTokens / kPageTokens];
 };
@@ -781,12 +757,9 @@ template <int HD, int G, bool F16, bool PERSIST, typename Sync>
 __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, const int32_t* pages, uint8_t* lds_raw,
                                Sync&& sync) {
     constexpr int CH = HD / 8;                 // 16-byte chunks per row
-    constexpr int NS = kThreads / CH;          // token slices in P.V
     constexpr int REC = G * HD + 2 * G;        // partial record floats
     AttnLds<HD, G>& L = *reinterpret_cast<AttnLds<HD, G>*>(lds_raw);
     auto& buf = L.buf;
-    auto& vt = L.vt;
-    auto& sc = L.sc;
     auto& red = L.red;
     auto& stat = L.stat;
     auto& pg = L.pg;
@@ -853,27 +826,44 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     for (int i = tid; i < n; i += kThreads)
         if ((i & (kPageTokens - 1)) == 0) pg[i / kPageTokens] = pages[(t0 + i) / kPageTokens];
     __syncthreads();
-    // Scores run on MFMA straight from registers: a wave takes 16-position
-    // blocks; lane (bn, bj) holds position bn's dims bj*HD/4 .. +HD/4 (KC
-    // 16-byte chunks). Its first block and the first V tile are in flight
-    // during the prologue.
+    // The split streams in 32-position blocks, one wave per block (blocks
+    // wave, wave + kWaves, ...). Lane (bn, bj) holds the k of positions bn
+    // and 16 + bn at dims bj*HD/4 .. +HD/4 (KC 16-byte chunks each), and VIT
+    // (position pair, 16-byte chunk) items of v. A wave's first block is in
+    // flight during the prologue.
     constexpr int KC = HD / 32;
+    constexpr int VIT = CH / 4;
     const int bn = lane & 15, bj = lane >> 4;
-    auto kload = [&](int blk, u4_t (&r)[KC]) {
-        const int tl = blk * 16 + bn;
-        if (tl < n) {
-            const uint16_t* src = a.kcache + ((size_t)(pg[blk] * a.hkv + kvh) * kPageTokens + (tl & 15)) * HD + bj * (HD / 4);
+    const int nblk = (n + 31) / 32;
+    auto kv_load = [&](int blk, u4_t (&kr)[2][KC], u4_t (&vr)[VIT][2]) {
+        const int b0 = blk * 32;
 #pragma unroll
-            for (int c = 0; c < KC; c++) r[c] = *reinterpret_cast<const u4_t*>(src + 8 * c);
-        } else {
+        for (int h = 0; h < 2; h++) {
+            const int tl = b0 + 16 * h + bn;
+            if (tl < n) {
+                const uint16_t* src =
+                    a.kcache + ((size_t)(pg[tl >> 4] * a.hkv + kvh) * kPageTokens + bn) * HD + bj * (HD / 4);
 #pragma unroll
-            for (int c = 0; c < KC; c++) r[c] = u4_t{0u, 0u, 0u, 0u};
+                for (int c = 0; c < KC; c++) kr[h][c] = *reinterpret_cast<const u4_t*>(src + 8 * c);
+            } else {
+#pragma unroll
+                for (int c = 0; c < KC; c++) kr[h][c] = u4_t{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; it++) {
+            const int item = it * 64 + lane, pp = item / CH, c8 = item % CH;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int tl = b0 + 2 * pp + e;
+                vr[it][e] = tl < n ? *reinterpret_cast<const u4_t*>(
+                                         a.vcache + ((size_t)(pg[tl >> 4] * a.hkv + kvh) * kPageTokens + (tl & 15)) * HD + c8 * 8)
+                                   : u4_t{0u, 0u, 0u, 0u};
+            }
         }
     };
-    u4_t kc[KC];
-    kload(wave, kc);
-    KvTile<HD, F16> vpre;
-    vpre.load(a.vcache, pg, a.hkv, kvh, 0, n, t0);
+    u4_t kr[2][KC], vr[VIT][2];
+    kv_load(wave, kr, vr);
     sync.phase(1);
     if (!sync()) return false;
     if constexpr (PERSIST) {
@@ -952,6 +942,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         for (int i = tid; i < G * HD; i += kThreads) buf[i / HD][i % HD] *= a.scale_log2;
     }
     if (hold_k) *reinterpret_cast<uint2*>(&L.kq[4 * pc]) = cur_k;
+    if (hold_v) *reinterpret_cast<uint2*>(&L.vq[4 * pc]) = cur_v;
     if (owner && (hold_k || hold_v)) {
         const int page = pg[(pos - t0) / kPageTokens], off = pos % kPageTokens;
         uint16_t* dst = (hold_k ? a.kcache : a.vcache) + ((size_t)(page * a.hkv + kvh) * kPageTokens + off) * HD;
@@ -960,16 +951,29 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     __syncthreads();
 
     sync.phase(3);
-    // -- scores S[head][position] = Q K^T (v_mfma_f32_16x16x32_f16). A = q
-    //    rows (heads; zero beyond G) in binary16 with log2(e)/sqrt(hd) folded
-    //    in, B = K^T from the lane's chunks; step c pairs lane group bj's
-    //    logical k 0..7 with dims bj*HD/4 + 8c .. +8 for both operands. A
-    //    bfloat16 cache is converted to binary16 (exact in binary16's normal
-    //    range). The current position's k comes from LDS, not the cache.
+    // -- flash decoding on MFMA (v_mfma_f32_16x16x32_f16), per wave and block:
+    //      S^T[pos][head] = K Q^T   A = k chunks, B = q (heads beyond G zero) in
+    //                               binary16 with log2(e)/sqrt(hd) folded in;
+    //                               step c pairs lane group bj's logical k
+    //                               0..7 with dims bj*HD/4 + 8c .. +8
+    //      online softmax per head (base 2), P rounded to binary16
+    //      O^T[dim][head] += V^T P^T  A = V^T from the wave's transposed LDS
+    //                               tile, B = P^T straight from the S^T
+    //                               accumulators: lane group bj's logical k
+    //                               0..7 are positions 4bj..4bj+3, 16+4bj..+3
+    //    The S^T / O^T orientation keeps each head in lane % 16. A bfloat16
+    //    cache is converted to binary16 (exact in binary16's normal range).
+    //    The current position's k and v come from LDS, not the cache.
     {
         typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
         typedef float f4v_t __attribute__((ext_vector_type(4)));
-        h8v_t qa[KC];
+        constexpr int NDB = HD / 16;   // 16-dim blocks of the output
+        auto to_f16x2 = [](uint32_t w) -> uint32_t {
+            if constexpr (F16) return w;
+            const _Float16 x = (_Float16)__uint_as_float(w << 16), y = (_Float16)__uint_as_float(w & 0xffff0000u);
+            return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        };
+        h8v_t qb[KC];
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const int d = bj * (HD / 4) + 8 * c;
@@ -978,124 +982,133 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 lo = *reinterpret_cast<const float4*>(&buf[bn][d]);
                 hi = *reinterpret_cast<const float4*>(&buf[bn][d + 4]);
             }
-            qa[c] = h8v_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+            qb[c] = h8v_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
                           (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
         }
-        auto to_f16x2 = [](uint32_t w) -> uint32_t {
-            if constexpr (F16) return w;
-            const _Float16 x = (_Float16)__uint_as_float(w << 16), y = (_Float16)__uint_as_float(w & 0xffff0000u);
-            return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        const int own = owner ? pos - t0 : -1;   // the current position within the split
+        uint32_t* vt = reinterpret_cast<uint32_t*>(&L.vts[wave][0][0]);   // [HD][kVtLd / 2] position pairs
+        auto v_stage = [&](int blk, const u4_t (&v)[VIT][2]) {
+#pragma unroll
+            for (int it = 0; it < VIT; it++) {
+                const int item = it * 64 + lane, pp = item / CH, c8 = item % CH;
+                const int tl = blk * 32 + 2 * pp;
+                const u4_t x = tl == own ? *reinterpret_cast<const u4_t*>(&L.vq[c8 * 8]) : v[it][0];
+                const u4_t y = tl + 1 == own ? *reinterpret_cast<const u4_t*>(&L.vq[c8 * 8]) : v[it][1];
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t xw = to_f16x2(dword_at(x, w)), yw = to_f16x2(dword_at(y, w));
+                    vt[(c8 * 8 + 2 * w) * (kVtLd / 2) + pp] = (xw & 0xffffu) | (yw << 16);
+                    vt[(c8 * 8 + 2 * w + 1) * (kVtLd / 2) + pp] = (xw >> 16) | (yw & 0xffff0000u);
+                }
+            }
         };
-        const int nblk = (n + 15) / 16;
-        const int own_blk = owner ? (pos - t0) / 16 : -1, own_bn = (pos - t0) & 15;
+        f4v_t acc[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; db++) acc[db] = f4v_t{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.f;   // per head bn; l_run is this lane's share
+        // The V^T tile is private to its wave and LDS executes a wave's
+        // accesses in order; the compiler barriers keep that order in the code.
+        if (wave < nblk) v_stage(wave, vr);
+        asm volatile("" ::: "memory");
         for (int blk = wave; blk < nblk; blk += kWaves) {   // wave-uniform
-            u4_t kn[KC];
-            kload(blk + kWaves, kn);
-            if (blk == own_blk && bn == own_bn) {
+            u4_t kn[2][KC], vn[VIT][2];
+            kv_load(blk + kWaves, kn, vn);
+            const int b0 = blk * 32;
+            f4v_t st[2];
 #pragma unroll
-                for (int c = 0; c < KC; c++) kc[c] = *reinterpret_cast<const u4_t*>(&L.kq[bj * (HD / 4) + 8 * c]);
+            for (int h = 0; h < 2; h++) {
+                if (b0 + 16 * h + bn == own) {
+#pragma unroll
+                    for (int c = 0; c < KC; c++) kr[h][c] = *reinterpret_cast<const u4_t*>(&L.kq[bj * (HD / 4) + 8 * c]);
+                }
+                st[h] = f4v_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < KC; c++) {
+                    const u4_t kb{to_f16x2(kr[h][c].x), to_f16x2(kr[h][c].y), to_f16x2(kr[h][c].z), to_f16x2(kr[h][c].w)};
+                    st[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, kb), qb[c], st[h], 0, 0, 0);
+                }
             }
-            f4v_t sacc{0.f, 0.f, 0.f, 0.f};
+            // positions b0 + 16h + 4bj + i; those past the split are masked
+            float bm = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < KC; c++) {
-                const u4_t kb{to_f16x2(kc[c].x), to_f16x2(kc[c].y), to_f16x2(kc[c].z), to_f16x2(kc[c].w)};
-                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], __builtin_bit_cast(h8v_t, kb), sacc, 0, 0, 0);
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (b0 + 16 * h + 4 * bj + i >= n) st[h][i] = -INFINITY;
+                    bm = fmaxf(bm, st[h][i]);
+                }
+            bm = xor32_max(xor16_max(bm));
+            const float m_new = fmaxf(m_run, bm);   // finite: every block holds a position
+            const float alpha = exp2f(m_run - m_new);
+            m_run = m_new;
+            float ps[8];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) ps[4 * h + i] = exp2f(st[h][i] - m_new);
+            float lsum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) lsum += ps[e];
+            l_run = l_run * alpha + lsum;
+            const h8v_t pb{(_Float16)ps[0], (_Float16)ps[1], (_Float16)ps[2], (_Float16)ps[3],
+                           (_Float16)ps[4], (_Float16)ps[5], (_Float16)ps[6], (_Float16)ps[7]};
+            const uint16_t* vrow = &L.vts[wave][0][0];
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                const uint16_t* r = vrow + (16 * db + bn) * kVtLd;
+                const uint2 lo = *reinterpret_cast<const uint2*>(r + 4 * bj);
+                const uint2 hi = *reinterpret_cast<const uint2*>(r + 16 + 4 * bj);
+                const u4_t va{lo.x, lo.y, hi.x, hi.y};
+                acc[db] *= alpha;
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, va), pb, acc[db], 0, 0, 0);
             }
-            const int tl = blk * 16 + bn;
+            asm volatile("" ::: "memory");
+            if (blk + kWaves < nblk) v_stage(blk + kWaves, vn);   // after this block's reads
+            asm volatile("" ::: "memory");
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int g = 4 * bj + i;
-                if (g < G && tl < n) sc[g][tl] = sacc[i];
-            }
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int c = 0; c < KC; c++) kc[c] = kn[c];
+                for (int c = 0; c < KC; c++) kr[h][c] = kn[h][c];
+        }
+        // -- merge the waves: per-head statistics, then O^T rows
+        l_run = xor32_sum(xor16_sum(l_run));
+        if (bj == 0 && bn < G) {
+            L.wst[wave][0][bn] = m_run;
+            L.wst[wave][1][bn] = l_run;
+        }
+        if (bn < G) {
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+                *reinterpret_cast<float4*>(&red[wave][bn * HD + 16 * db + 4 * bj]) =
+                    float4{acc[db][0], acc[db][1], acc[db][2], acc[db][3]};
         }
         __syncthreads();
-    }
-
-    sync.phase(4);
-    // -- softmax statistics per head
-    for (int g = wave; g < G; g += kWaves) {
-        float m = -INFINITY;
-        for (int tl = lane; tl < n; tl += 64) m = fmaxf(m, sc[g][tl]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int tl = lane; tl < n; tl += 64) {
-            const float p = exp2f(sc[g][tl] - m);
-            sc[g][tl] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        if (lane == 0) { stat[0][g] = m; stat[1][g] = l; }
-    }
-    __syncthreads();
-
-    sync.phase(5);
-    // -- o[g] = sum_t p[g][t] v[t]
-    const int ch = tid % CH, sl = tid / CH;
-    float o[G][8];
+        if (tid < G) {
+            float mx = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < G; g++)
+            for (int w = 0; w < kWaves; w++) mx = fmaxf(mx, L.wst[w][0][tid]);
+            float lt = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; i++) o[g][i] = 0.f;
-    KvTile<HD, F16> vcur = vpre;
-    for (int c0 = 0; c0 < n; c0 += kTile) {
-        KvTile<HD, F16> vnext;
-        vnext.load(a.vcache, pg, a.hkv, kvh, c0 + kTile, n, t0);
-        if (c0 > 0) __syncthreads();
-        vcur.store(vt);
-        vcur = vnext;
-        if (owner && pos - t0 >= c0 && pos - t0 < c0 + kTile) {   // uniform across the workgroup
-            __syncthreads();
-            if (hold_v) *reinterpret_cast<uint2*>(&vt[pos - t0 - c0][4 * pc]) = cur_v;
+            for (int w = 0; w < kWaves; w++) {
+                const float wgt = L.wst[w][0][tid] == -INFINITY ? 0.f : exp2f(L.wst[w][0][tid] - mx);
+                L.wst[w][0][tid] = wgt;
+                lt += wgt * L.wst[w][1][tid];
+            }
+            stat[0][tid] = mx;
+            stat[1][tid] = lt;
         }
         __syncthreads();
-        const int lim = min(kTile, n - c0);
-        for (int j = sl; j < lim; j += NS) {
-            const u4_t vw = *reinterpret_cast<const u4_t*>(&vt[j][ch * 8]);
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t w = dword_at(vw, i);
-                v[2 * i] = kv_decode<F16>(w & 0xffffu);
-                v[2 * i + 1] = kv_decode<F16>(w >> 16);
-            }
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = sc[g][c0 + j];
-#pragma unroll
-                for (int i = 0; i < 8; i++) o[g][i] = fmaf(p, v[i], o[g][i]);
-            }
-        }
     }
     sync.phase(6);
     const bool direct = a.n_splits == 1;
     float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
-    // the slices of one wave (lanes CH apart) reduce in registers, the waves in LDS
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float t = o[g][i];
-            if constexpr (CH == 8) t += dpp_f<0x128>(t);   // row_ror:8 = lane ^ 8 within a row
-            t = xor16_sum(t);
-            o[g][i] = xor32_sum(t);
-        }
-    if (lane < CH) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int i = 0; i < 8; i += 4)
-                *reinterpret_cast<float4*>(&red[wave][g * HD + ch * 8 + i]) =
-                    float4{o[g][i], o[g][i + 1], o[g][i + 2], o[g][i + 3]};
-    }
-    __syncthreads();
     for (int idx = tid; idx < G * HD; idx += kThreads) {
-        float acc = 0.f;
+        const int g = idx / HD;
+        float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) acc += red[w][idx];
-        if (direct) st_agent(a.out + (size_t)kvh * G * HD + idx, acc / stat[1][idx / HD]);
-        else st_agent(rec + idx, acc);
+        for (int w = 0; w < kWaves; w++) o = fmaf(L.wst[w][0][g], red[w][idx], o);
+        if (direct) st_agent(a.out + (size_t)kvh * G * HD + idx, o / stat[1][g]);
+        else st_agent(rec + idx, o);
     }
     if (direct) return true;
     if (tid < G) {
@@ -1114,7 +1127,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     constexpr int GPW = (G + kWaves - 1) / kWaves;   // heads per wave in the statistics
     constexpr int SPL = kMaxSplits / 64;               // splits per lane
     const float* base = a.part + (size_t)kvh * a.n_splits * REC;
-    float* swt = &sc[0][0];                            // [G][n_splits] weights (scores are dead)
+    float* swt = L.swt;                                // [G][n_splits] weights
     float mv[GPW][SPL], lv[GPW][SPL];
 #pragma unroll
     for (int gi = 0; gi < GPW; gi++)

@@ -8,14 +8,19 @@ namespace ribn {
 
 constexpr int kPageTokens = 16;   // KV page size (crates/qwen/src/gguf.rs:16)
 constexpr int kMaxSplits = 128;   // split-K limit of decode attention
-constexpr int kMaxSplitTokens = 512;   // positions one attention workgroup covers
+constexpr int kMaxSplitTokens = 2048;   // positions one attention workgroup covers
 
-// Decode-attention splits for a context of `ctx` positions: about 64 positions
-// per workgroup, a power of two, at most kMaxSplits (a split then covers at
-// most kMaxSplitTokens positions for contexts up to kMaxSplits * kMaxSplitTokens).
+// Decode-attention splits for a context of `ctx` positions, a power of two
+// (measured on MI355X for head_dim 64 and 128, 1 to 8 query heads per KV head):
+// one workgroup up to 128 positions; at least 4 and about 128 positions each up
+// to 2048; about 256 each up to 8192 and about 1024 beyond, at most kMaxSplits
+// (a split then covers at most kMaxSplitTokens positions for contexts up to
+// kMaxSplits * kMaxSplitTokens).
 __host__ __device__ inline int splits_for_ctx(int ctx) {
-    const int want = (ctx + 63) / 64;
-    int s = 1;
+    if (ctx <= 128) return 1;
+    const int per = ctx <= 2048 ? 128 : ctx <= 8192 ? 256 : 1024;
+    const int want = (ctx + per - 1) / per;
+    int s = 4;
     while (s < want && s < kMaxSplits) s <<= 1;
     return s;
 }
