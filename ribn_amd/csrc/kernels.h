@@ -209,6 +209,8 @@ struct PrefillRows {
     uint16_t* vcache;
 };
 
+constexpr int kGemmTileN = 128;   // weight rows per prefill-GEMM workgroup
+inline int gemm_tiles(int rows) { return (rows + kGemmTileN - 1) / kGemmTileN; }
 size_t prefill_gemm_lds_bytes();
 // split count launch_prefill_gemm would use for this GEMM (partials need ksplit * m * ldy floats)
 int prefill_gemm_splits(int m, int k, int n_tiles);

@@ -632,7 +632,7 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
         for (const PrefillSeg& sg : segs) {
             g.seg[g.nseg] = sg;
             g.seg[g.nseg].tile0 = tiles;
-            tiles += (int)((sg.w.rows + 127) / 128);
+            tiles += gemm_tiles((int)sg.w.rows);
             g.nseg++;
         }
         g.ksplit = prefill_gemm_splits(m, k, tiles);
@@ -714,7 +714,7 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
         for (const PrefillSeg& sg : segs) {
             g.seg[g.nseg] = sg;
             g.seg[g.nseg].tile0 = tiles;
-            tiles += (int)((sg.w.rows + 127) / 128);
+            tiles += gemm_tiles((int)sg.w.rows);
             g.nseg++;
         }
         g.ksplit = prefill_gemm_splits(n, k, tiles);
@@ -1031,7 +1031,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         // split-K partials: the largest split x ldy over the chunk's GEMMs
         const int ldq = qd + 2 * kd;
         auto need = [&](int k, int ldy, int tiles) { return (size_t)prefill_gemm_splits(M->chunk, k, tiles) * ldy; };
-        const int t_qkv = (qd + 127) / 128 + 2 * ((kd + 127) / 128), t_h = (M->H + 127) / 128, t_gu = 2 * ((M->F + 127) / 128);
+        const int t_qkv = gemm_tiles(qd) + 2 * gemm_tiles(kd), t_h = gemm_tiles(M->H), t_gu = 2 * gemm_tiles(M->F);
         size_t per_row = std::max(std::max(need(M->H, ldq, t_qkv), need(qd, M->H, t_h)),
                                   std::max(need(M->H, 2 * M->F, t_gu), need(M->F, M->H, t_h)));
         M->p_part_floats = per_row * c;
@@ -1800,7 +1800,7 @@ extern "C" int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t* blocks, uint
     g.x = dx16; g.m = (int)m; g.k = (int)k; g.y = dy; g.ldy = (int)rows; g.mode = MV_STORE;
     g.nseg = 1;
     g.seg[0].w = q;
-    g.ksplit = prefill_gemm_splits((int)m, (int)k, (int)((rows + 127) / 128));
+    g.ksplit = prefill_gemm_splits((int)m, (int)k, gemm_tiles((int)rows));
     if (g.ksplit > 1) HIPCHK(S.alloc(&g.part, sizeof(float) * g.ksplit * m * rows));
     HIPCHK(launch_prefill_gemm(g, nullptr));
     HIPCHK(hipMemcpy(y, dy, sizeof(float) * m * rows, hipMemcpyDeviceToHost));

@@ -4,9 +4,10 @@
 // 2360; the reference batches 8 rows through warp GEMVs, this build uses MFMA).
 //
 //  * prefill_gemm: Y[M][N] = X[M][K] deq(W)^T. X is binary16 (the RMSNorm'd or
-//    activation rows), W stays in its GGUF planes and each 256-wide K slice of a
-//    128-row tile is dequantized (exactly as dequantize_block, then rounded to
-//    binary16) into LDS; v_mfma_f32_16x16x32_f16 accumulates in fp32.
+//    activation rows), W stays in its GGUF planes and every lane dequantizes
+//    its weight values straight into MFMA operand registers (exactly as
+//    dequantize_block, then rounded to binary16); v_mfma_f32_16x16x32_f16
+//    accumulates in fp32.
 //  * rows_rms_f16, embed_rows, qk_rope_append, prefill_attention, silu_mul_f16:
 //    the per-row steps around the GEMMs, same equations as the decode kernels.
 #include <hip/hip_runtime.h>
@@ -24,16 +25,9 @@ typedef unsigned u4v_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
 constexpr int kTileM = 128;   // chunk rows per workgroup
-constexpr int kTileN = 128;   // weight rows per workgroup
 constexpr int kTileK = 128;   // half a Q4_K / Q6_K super-block, four Q8_0 blocks
 #ifndef RIBN_PG_PAD
 #define RIBN_PG_PAD 8
-#endif
-#ifndef RIBN_PG_REMAP
-#define RIBN_PG_REMAP 0
-#endif
-#ifndef RIBN_PG_DEPTH
-#define RIBN_PG_DEPTH 1
 #endif
 constexpr int kLdsRow = kTileK + RIBN_PG_PAD;   // halves per LDS row (padded against bank conflicts)
 
@@ -44,306 +38,269 @@ __device__ __forceinline__ float canon(uint32_t b) {
 }
 __device__ __forceinline__ uint16_t f2h_bits(float f) { return __half_as_ushort(__float2half_rn(f)); }
 
-// Dequantize 64 consecutive values of one weight row into LDS as binary16:
-// values [128 kt + 64 q, +64) of the row (kt = 128-wide K tile, q = quarter of
-// it), computed exactly as dequantize_block (gguf/src/lib.rs:584-649) and then
-// rounded to binary16.
-// The bytes of one quarter are fetched into registers one K tile ahead
-// (QuarterRaw<T>::fetch) and converted into LDS when that tile is staged
-// (QuarterRaw<T>::convert), so the weight loads are in flight during the MFMA
-// phase of the previous tile.
+// Weight fragments straight from the GGUF planes. In a 128-wide K tile, lane
+// (bn, bj) of a 16-row weight block dequantizes 32 values of row bn into the
+// MFMA B operand of the four 32-wide K steps (8 values each): the values it
+// can load contiguously. Which 8 values step ks gets is fixed per type by
+// xoff(ks, bj), the offset of the matching 8 contiguous X values in the tile
+// (the contraction does not depend on how K is ordered inside a step, only on
+// both operands using the same order). Each value follows dequantize_block
+// (gguf/src/lib.rs:584-649) exactly, then rounded to binary16: the quant
+// integer is built exactly as binary16 (1024 + q with v_perm_b32, minus the
+// bias in one packed add for two values) and v_fma_mix computes the fp32
+// result from it and rounds that to binary16 (about two VALU instructions per
+// value). The raw bytes of the next K tile are fetched while the current one
+// is multiplied.
 template <int T>
-struct QuarterRaw;
+struct WFrag;
 
-__device__ __forceinline__ void store16(uint16_t* dst, const uint32_t (&o)[8]) {
-    u4v_t* out = reinterpret_cast<u4v_t*>(dst);
-    out[0] = u4v_t{o[0], o[1], o[2], o[3]};
-    out[1] = u4v_t{o[4], o[5], o[6], o[7]};
+typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
+typedef float f2v_t __attribute__((ext_vector_type(2)));
+// two fp32 values -> binary16 pair, round to nearest even (v_cvt_pk_f16_f32)
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v_t{a, b}), h2v_t));
 }
-__device__ __forceinline__ uint32_t lane_of(const u4v_t& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+// Four small unsigned integers (the bytes of v, each < 1024) -> two binary16
+// pairs holding 1024 + byte, exact (0x64 is the high byte of 1024.0):
+// lo = bytes 0, 1, hi = bytes 2, 3 (v_perm_b32 with 0x64 bytes from the other source).
+__device__ __forceinline__ h2v_t bias1024_lo(uint32_t v) {
+    return __builtin_bit_cast(h2v_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
+}
+__device__ __forceinline__ h2v_t bias1024_hi(uint32_t v) {
+    return __builtin_bit_cast(h2v_t, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
+}
+// round16(round32(q * g + c)) for a pair of exact binary16 integers q: the
+// reference's fp32 result rounded to binary16 (v_fma_mixlo/mixhi_f16)
+__device__ __forceinline__ uint32_t mix2(h2v_t q, float g, float c) {
+    const h2v_t r{(_Float16)__builtin_fmaf((float)q[0], g, c), (_Float16)__builtin_fmaf((float)q[1], g, c)};
+    return __builtin_bit_cast(uint32_t, r);
+}
 
 template <>
-struct QuarterRaw<12> {
-    // group pair p = 2 (kt % 2) + q of block kt / 2: group 2p = low nibbles of qs
-    // bytes 32p..32p+31, group 2p+1 = their high nibbles; scale dword p holds
-    // sc(2p), sc(2p+1), m(2p), m(2p+1)
+struct WFrag<12> {
+    // Q4_K: the tile's group pair p = 2 (kt % 2) + bj / 2 of block kt / 2; the
+    // lane's 16 bytes are qs[32p + 16 (bj % 2) ..]: low nibbles = values
+    // 64 (bj/2) + 16 (bj%2) + b of the tile, high nibbles = the same + 32.
+    // Scale dword p = sc(2p), sc(2p+1), m(2p), m(2p+1).
     uint32_t dd, s;
-    u4v_t qv[2];
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int q) {
+    u4v_t qv;
+    __device__ static __forceinline__ int xoff(int ks, int j) { return 64 * (j >> 1) + 16 * (j & 1) + 8 * (ks & 1) + 32 * (ks >> 1); }
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
         const size_t bi = row * w.nb + (kt >> 1);
-        const int p = 2 * (kt & 1) + q;
+        const int p = 2 * (kt & 1) + (j >> 1);
         dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
         s = reinterpret_cast<const uint32_t*>(w.b + bi * 16)[p];
-        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p);
-        qv[0] = qs[0];
-        qv[1] = qs[1];
+        qv = *reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p + 16 * (j & 1));
     }
-    __device__ __forceinline__ void convert(uint16_t* dst) const {
+    // value = round16(fma(q, sc*d, -m*dmin)): g * q is exact in fp32 (d has
+    // 11 significant bits, sc 6, q 4), so the fma rounds once, as the
+    // reference's multiply-then-subtract does
+    __device__ __forceinline__ h8_t frag(int ks) const {
         const float d = canon(dd), dmin = canon(dd >> 16);
-        const float g0 = __fmul_rn(d, (float)(s & 0xffu)), g1 = __fmul_rn(d, (float)((s >> 8) & 0xffu));
-        const float m0 = __fmul_rn(dmin, (float)((s >> 16) & 0xffu)), m1 = __fmul_rn(dmin, (float)(s >> 24));
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            uint32_t lo[8], hi[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t v = lane_of(qv[c], j);
-                uint32_t a[4], bb[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    a[e] = f2h_bits(__fsub_rn(__fmul_rn(g0, (float)((v >> (8 * e)) & 15u)), m0));
-                    bb[e] = f2h_bits(__fsub_rn(__fmul_rn(g1, (float)((v >> (8 * e + 4)) & 15u)), m1));
-                }
-                lo[2 * j] = a[0] | (a[1] << 16);
-                lo[2 * j + 1] = a[2] | (a[3] << 16);
-                hi[2 * j] = bb[0] | (bb[1] << 16);
-                hi[2 * j + 1] = bb[2] | (bb[3] << 16);
-            }
-            store16(dst + 16 * c, lo);
-            store16(dst + 32 + 16 * c, hi);
-        }
+        const int hi = ks >> 1;   // 0: low nibbles (group 2p), 1: high nibbles (group 2p + 1)
+        const float g = __fmul_rn(d, (float)((s >> (8 * hi)) & 0xffu));
+        const float m = __fmul_rn(dmin, (float)((s >> (16 + 8 * hi)) & 0xffu));
+        const uint32_t w0 = (ks & 1) ? qv.z : qv.x, w1 = (ks & 1) ? qv.w : qv.y;
+        const uint32_t n0 = (w0 >> (4 * hi)) & 0x0f0f0f0fu, n1 = (w1 >> (4 * hi)) & 0x0f0f0f0fu;
+        const h2v_t k1024 = h2v_t{(_Float16)1024.0f, (_Float16)1024.0f};
+        const u4v_t o{mix2(bias1024_lo(n0) - k1024, g, -m), mix2(bias1024_hi(n0) - k1024, g, -m),
+                      mix2(bias1024_lo(n1) - k1024, g, -m), mix2(bias1024_hi(n1) - k1024, g, -m)};
+        return __builtin_bit_cast(h8_t, o);
     }
 };
 
 template <>
-struct QuarterRaw<14> {
-    // chunk h = kt % 2 of block kt / 2 (ql bytes 64h.., qh bytes 32h..); value
-    // 32v + l of the chunk: ((ql[32 (v%2) + l] >> 4 (v/2)) & 15) | (((qh[l] >> 2v) & 3) << 4),
-    // minus 32, times d * sc(8h + 2v + l/16); the quarter q holds v = 2q, 2q + 1.
-    // Sub-block scale s sits at c-plane byte 2c + slot, c = 4 (s/8) + s%4, slot = (s/4) % 2.
-    uint32_t d16, sc4;   // d; the quarter's four sub-block scales (int8, order vv * 2 + lc)
-    int q;
-    u4v_t ql[4], qh[2];
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int qq) {
+struct WFrag<14> {
+    // Q6_K: chunk h = kt % 2 of block kt / 2 (ql bytes 64h.., qh bytes 32h..);
+    // value 32v + l of the chunk is ((ql[32 (v%2) + l] >> 4 (v/2)) & 15) |
+    // (((qh[l] >> 2v) & 3) << 4), minus 32, times d * sc(8h + 2v + l/16).
+    // Lane bj holds l = 8 bj .. 8 bj + 7 for v = 0..3 (step ks = v). Sub-block
+    // scale s sits at c-plane byte 2c + slot, c = 4 (s/8) + s%4, slot = (s/4) % 2:
+    // for s = 8h + 2v + bj/2 that is byte 8h + 4 (v%2) + 2 (bj/2) + v/2.
+    uint32_t d16, sc01, sc23;   // scale bytes (v=0, v=2) and (v=1, v=3)
+    uint2 ql0, ql1, qh;
+    __device__ static __forceinline__ int xoff(int ks, int j) { return 32 * ks + 8 * j; }
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
         const size_t bi = row * w.nb + (kt >> 1);
         const int h = kt & 1;
-        q = qq;
         d16 = *reinterpret_cast<const uint16_t*>(w.d + bi * 2);
-        const uint8_t* sp = w.c + bi * 16;
-        sc4 = 0;
-#pragma unroll
-        for (int vv = 0; vv < 2; vv++)
-#pragma unroll
-            for (int lc = 0; lc < 2; lc++) {
-                const int sb = 8 * h + 2 * (2 * qq + vv) + lc;
-                sc4 |= (uint32_t)sp[2 * (4 * (sb / 8) + sb % 4) + (sb / 4) % 2] << (8 * (2 * vv + lc));
-            }
-        const u4v_t* ql4 = reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 64 * h);
-        const u4v_t* qh4 = reinterpret_cast<const u4v_t*>(w.b + bi * 64 + 32 * h);
-#pragma unroll
-        for (int i = 0; i < 4; i++) ql[i] = ql4[i];
-        qh[0] = qh4[0];
-        qh[1] = qh4[1];
+        const uint8_t* sp = w.c + bi * 16 + 8 * h + 2 * (j >> 1);
+        sc01 = *reinterpret_cast<const uint16_t*>(sp);
+        sc23 = *reinterpret_cast<const uint16_t*>(sp + 4);
+        ql0 = *reinterpret_cast<const uint2*>(w.a + bi * 128 + 64 * h + 8 * j);
+        ql1 = *reinterpret_cast<const uint2*>(w.a + bi * 128 + 64 * h + 32 + 8 * j);
+        qh = *reinterpret_cast<const uint2*>(w.b + bi * 64 + 32 * h + 8 * j);
     }
-    __device__ __forceinline__ void convert(uint16_t* dst) const {
+    // value = round16(round32(d*sc * (q - 32))), q - 32 exact in binary16
+    __device__ __forceinline__ h8_t frag(int v) const {
         const float d = canon(d16);
-#pragma unroll
-        for (int vv = 0; vv < 2; vv++) {
-            const int v = 2 * q + vv;
-#pragma unroll
-            for (int lc = 0; lc < 2; lc++) {
-                const float gsc = __fmul_rn(d, (float)(int8_t)(sc4 >> (8 * (2 * vv + lc))));
-                const u4v_t qlv = ql[2 * vv + lc], qhv = qh[lc];
-                uint32_t o[8];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t lw = lane_of(qlv, j), hw = lane_of(qhv, j);
-                    uint32_t e[4];
-#pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        const int qq = (int)((((lw >> (8 * b)) >> (4 * q)) & 15u) | ((((hw >> (8 * b)) >> (2 * v)) & 3u) << 4)) - 32;
-                        e[b] = f2h_bits(__fmul_rn(gsc, (float)qq));
-                    }
-                    o[2 * j] = e[0] | (e[1] << 16);
-                    o[2 * j + 1] = e[2] | (e[3] << 16);
-                }
-                store16(dst + 32 * vv + 16 * lc, o);
-            }
-        }
+        const uint32_t scb = (v & 1) ? sc23 : sc01;
+        const float gsc = __fmul_rn(d, (float)(int8_t)(scb >> (8 * (v >> 1))));
+        const uint2 l = (v & 1) ? ql1 : ql0;
+        // bytes of q (0..63) for positions e = 0..3 (x) and 4..7 (y)
+        const uint32_t qx = ((l.x >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((qh.x >> (2 * v)) & 0x03030303u) << 4);
+        const uint32_t qy = ((l.y >> (4 * (v >> 1))) & 0x0f0f0f0fu) | (((qh.y >> (2 * v)) & 0x03030303u) << 4);
+        const h2v_t k1056 = h2v_t{(_Float16)1056.0f, (_Float16)1056.0f};
+        const u4v_t o{mix2(bias1024_lo(qx) - k1056, gsc, 0.f), mix2(bias1024_hi(qx) - k1056, gsc, 0.f),
+                      mix2(bias1024_lo(qy) - k1056, gsc, 0.f), mix2(bias1024_hi(qy) - k1056, gsc, 0.f)};
+        return __builtin_bit_cast(h8_t, o);
     }
 };
 
 template <>
-struct QuarterRaw<8> {
-    // Q8_0 blocks 4 kt + 2q and 4 kt + 2q + 1; past the row's end (k % 128 != 0): zeros
-    uint32_t d16[2];
-    u4v_t qv[2][2];
-    bool present[2];
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int q) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int qb = 4 * kt + 2 * q + b;
-            present[b] = qb < (int)w.nb;
-            d16[b] = 0u;
-            qv[b][0] = qv[b][1] = u4v_t{0u, 0u, 0u, 0u};
-            if (present[b]) {
-                const size_t bi = row * w.nb + (size_t)qb;
-                d16[b] = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
-                const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
-                qv[b][0] = qs[0];
-                qv[b][1] = qs[1];
-            }
+struct WFrag<8> {
+    // Q8_0: lane bj holds block 4 kt + bj (step ks = its bytes 8 ks ..);
+    // past the row's end (k % 128 != 0): zeros
+    uint32_t d16;
+    u4v_t qv[2];
+    __device__ static __forceinline__ int xoff(int ks, int j) { return 32 * j + 8 * ks; }
+    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
+        const int qb = 4 * kt + j;
+        d16 = 0u;
+        qv[0] = qv[1] = u4v_t{0u, 0u, 0u, 0u};
+        if (qb < (int)w.nb) {
+            const size_t bi = row * w.nb + (size_t)qb;
+            d16 = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
+            const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
+            qv[0] = qs[0];
+            qv[1] = qs[1];
         }
     }
-    __device__ __forceinline__ void convert(uint16_t* dst) const {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            uint32_t o[2][8];
-            const float d = canon(d16[b]);
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t v = lane_of(qv[b][c], j);
-                    uint32_t e[4];
-#pragma unroll
-                    for (int k = 0; k < 4; k++) e[k] = present[b] ? f2h_bits(__fmul_rn(d, (float)(int8_t)(v >> (8 * k)))) : 0u;
-                    o[c][2 * j] = e[0] | (e[1] << 16);
-                    o[c][2 * j + 1] = e[2] | (e[3] << 16);
-                }
-            }
-            store16(dst + 32 * b, o[0]);
-            store16(dst + 32 * b + 16, o[1]);
-        }
+    // value = round16(d * q) (d * q is exact in fp32), q exact in binary16
+    // (int8 as q + 128 unsigned)
+    __device__ __forceinline__ h8_t frag(int ks) const {
+        const float d = canon(d16);
+        const u4v_t& v = qv[ks >> 1];
+        const uint32_t w0 = ((ks & 1) ? v.z : v.x) ^ 0x80808080u, w1 = ((ks & 1) ? v.w : v.y) ^ 0x80808080u;
+        const h2v_t k1152 = h2v_t{(_Float16)1152.0f, (_Float16)1152.0f};
+        const u4v_t o{mix2(bias1024_lo(w0) - k1152, d, 0.f), mix2(bias1024_hi(w0) - k1152, d, 0.f),
+                      mix2(bias1024_lo(w1) - k1152, d, 0.f), mix2(bias1024_hi(w1) - k1152, d, 0.f)};
+        return __builtin_bit_cast(h8_t, o);
     }
 };
 
-// Workgroup tile: 128 chunk rows x 128 weight rows of one segment; wave w owns
-// weight rows 32w..32w+31 of the tile (two 16-column MFMA blocks) for all 128
-// chunk rows (eight 16-row blocks): 16 accumulators of 4 floats. K runs in
-// tiles of 128 (X slice and dequantized W slice in LDS, 70 KB: two workgroups
-// per CU, so one stages while the other multiplies).
+// Workgroup tile: MT chunk rows x kGemmTileN (128) weight rows of one segment;
+// wave w owns weight rows 32w..32w+31 of the tile (two 16-row blocks, whose B
+// fragments it dequantizes itself) for all MT chunk rows (MT/16 blocks of A
+// fragments from the X tile in LDS). K runs in tiles of 128; the X slice is
+// staged through two LDS buffers (MT x 128 binary16 each, one barrier per
+// tile) and the next tile's X chunks and raw weight bytes are fetched into
+// registers during the current tile's MFMAs. Two workgroups share a CU.
 // MFMA 16x16x32 f16 operand layout (lane l): A[m = l%16][k = 8(l/16) .. +8],
 // B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
 // MT (128 or 32) is the workgroup's chunk rows: 32 for batched decode rows,
 // where a 128-row tile would mostly multiply padding.
-template <int TA, int TB, int MT>
-__global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
-    constexpr int MB = MT / 16;                // 16-row MFMA blocks
+template <int T, int MT>
+__device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg& sg, int m0, int n0, int kt0, int kt1,
+                                          int z, uint16_t* xs) {
+    constexpr int MB = MT / 16;                // 16-row blocks of chunk rows
+    constexpr int NB = kGemmTileN / 64;        // 16-row weight blocks per wave
     constexpr int XR = MT * 16 / kGemmThreads; // X chunks per thread per K tile
-    extern __shared__ __attribute__((aligned(16))) uint16_t plds[];
-    uint16_t* xs = plds;                       // [MT][kLdsRow]
-    uint16_t* ws = plds + MT * kLdsRow;        // [kTileN][kLdsRow]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int si = 0;
-    if (g.nseg > 1 && (int)blockIdx.x >= g.seg[1].tile0) si = 1;
-    if (g.nseg > 2 && (int)blockIdx.x >= g.seg[2].tile0) si = 2;
-    const PrefillSeg sg = g.seg[si];
-    const int m0 = blockIdx.y * MT, n0 = ((int)blockIdx.x - sg.tile0) * kTileN;
+    const int bn = lane & 15, bj = lane >> 4;
     const int n_rows = (int)sg.w.rows;
-    f4_t acc[MB][2];
+    f4_t acc[MB][NB];
 #pragma unroll
-    for (int i = 0; i < MB; i++) {
-        acc[i][0] = f4_t{0.f, 0.f, 0.f, 0.f};
-        acc[i][1] = f4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    const int n_kt = (g.k + kTileK - 1) / kTileK;
-    const int ks = max(1, g.ksplit), z = blockIdx.z;
-    const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
-    // dequant: row of the tile, quarter of the K tile
-    const int wr = RIBN_PG_REMAP ? 32 * wave + (lane & 31) : tid >> 1, wq = RIBN_PG_REMAP ? lane >> 5 : tid & 1;
-    const size_t wrow = (size_t)min(n0 + wr, n_rows - 1);
-    const bool use_b = si == 2 && TB != TA;
-    // K tiles in flight in registers: X slice (128 rows x 128 halves = 2048
-    // 16-byte chunks, 8 per thread) and this thread's weight quarter
-    struct Stage {
-        u4v_t xr[XR];
-        QuarterRaw<TA> ra;
-        QuarterRaw<TB> rb;
-    };
-    auto fetch = [&](Stage& st, int kt) {
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) acc[i][nb] = f4_t{0.f, 0.f, 0.f, 0.f};
+    size_t wrow[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) wrow[nb] = (size_t)min(n0 + 16 * NB * wave + 16 * nb + bn, n_rows - 1);
+    u4v_t xr[XR];
+    WFrag<T> w0[NB], w1[NB];   // raw weight bytes of tiles kt and kt + 1
+    auto fetch_x = [&](int kt) {
 #pragma unroll
         for (int j = 0; j < XR; j++) {
             const int idx = j * kGemmThreads + tid;
             const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
-            st.xr[j] = u4v_t{0u, 0u, 0u, 0u};
-            if (m0 + r < g.m && col < g.k) st.xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
-        }
-        if constexpr (TB != TA) {
-            if (use_b) st.rb.fetch(sg.w, wrow, kt, wq);
-            else st.ra.fetch(sg.w, wrow, kt, wq);
-        } else {
-            st.ra.fetch(sg.w, wrow, kt, wq);
+            xr[j] = u4v_t{0u, 0u, 0u, 0u};
+            if (m0 + r < g.m && col < g.k) xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
         }
     };
-    auto stage = [&](const Stage& st) {
+    auto store_x = [&](uint16_t* buf) {
 #pragma unroll
         for (int j = 0; j < XR; j++) {
             const int idx = j * kGemmThreads + tid;
-            *reinterpret_cast<u4v_t*>(xs + (idx >> 4) * kLdsRow + (idx & 15) * 8) = st.xr[j];
-        }
-        if constexpr (TB != TA) {
-            if (use_b) st.rb.convert(ws + wr * kLdsRow + 64 * wq);
-            else st.ra.convert(ws + wr * kLdsRow + 64 * wq);
-        } else {
-            st.ra.convert(ws + wr * kLdsRow + 64 * wq);
+            *reinterpret_cast<u4v_t*>(buf + (idx >> 4) * kLdsRow + (idx & 15) * 8) = xr[j];
         }
     };
-    auto multiply = [&]() {
+    auto fetch_w = [&](WFrag<T> (&wf)[NB], int kt) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) wf[nb].fetch(sg.w, wrow[nb], kt, bj);
+    };
+    if (kt0 < kt1) {
+        fetch_x(kt0);
+        fetch_w(w0, kt0);
+        store_x(xs);
+        if (kt0 + 1 < kt1) fetch_x(kt0 + 1);
+        __syncthreads();
+    }
+    for (int kt = kt0; kt < kt1; kt++) {
+        if (kt + 1 < kt1) fetch_w(w1, kt + 1);
+        const uint16_t* xb = xs + (size_t)((kt - kt0) & 1) * MT * kLdsRow;
 #pragma unroll
         for (int ks = 0; ks < kTileK / 32; ks++) {
-            const int kk = ks * 32 + 8 * (lane >> 4);
-            h8_t b[2];
+            const int kk = WFrag<T>::xoff(ks, bj);
+            h8_t a[MB];
 #pragma unroll
-            for (int nb = 0; nb < 2; nb++)
-                b[nb] = *reinterpret_cast<const h8_t*>(ws + (32 * wave + 16 * nb + (lane & 15)) * kLdsRow + kk);
+            for (int mb = 0; mb < MB; mb++) a[mb] = *reinterpret_cast<const h8_t*>(xb + (16 * mb + bn) * kLdsRow + kk);
 #pragma unroll
-            for (int mb = 0; mb < MB; mb++) {
-                const h8_t a = *reinterpret_cast<const h8_t*>(xs + (16 * mb + (lane & 15)) * kLdsRow + kk);
-                acc[mb][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[0], acc[mb][0], 0, 0, 0);
-                acc[mb][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[1], acc[mb][1], 0, 0, 0);
+            for (int nb = 0; nb < NB; nb++) {
+                const h8_t b = w0[nb].frag(ks);
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mb], b, acc[mb][nb], 0, 0, 0);
             }
         }
-    };
-#if RIBN_PG_DEPTH == 2
-    // two tiles ahead: the loads of tile kt + 2 are issued while tile kt is multiplied
-    Stage s0, s1;
-    if (kt0 < kt1) fetch(s0, kt0);
-    if (kt0 + 1 < kt1) fetch(s1, kt0 + 1);
-    for (int kt = kt0; kt < kt1; kt += 2) {
-        __syncthreads();   // the previous tile's MFMA reads are done
-        stage(s0);
-        __syncthreads();
-        if (kt + 2 < kt1) fetch(s0, kt + 2);
-        multiply();
-        if (kt + 1 >= kt1) break;
-        __syncthreads();
-        stage(s1);
-        __syncthreads();
-        if (kt + 3 < kt1) fetch(s1, kt + 3);
-        multiply();
-    }
-#else
-    Stage s0;
-    if (kt0 < kt1) fetch(s0, kt0);
-    for (int kt = kt0; kt < kt1; kt++) {
-        __syncthreads();   // the previous tile's MFMA reads are done
-        stage(s0);
-        __syncthreads();
-        if (kt + 1 < kt1) fetch(s0, kt + 1);
-        multiply();
-    }
-#endif
-    // epilogue: C[m][n] of block (mb, nb): m = 16 mb + 4 (lane / 16) + i, n = 16 nb + lane % 16
+        if (kt + 1 < kt1) {
+            // the other buffer was last read in the previous tile, before its barrier
+            store_x(xs + (size_t)((kt + 1 - kt0) & 1) * MT * kLdsRow);
+            if (kt + 2 < kt1) fetch_x(kt + 2);
 #pragma unroll
-    for (int nb = 0; nb < 2; nb++) {
-        const int n = n0 + 32 * wave + 16 * nb + (lane & 15);
+            for (int nb = 0; nb < NB; nb++) w0[nb] = w1[nb];
+        }
+        __syncthreads();
+    }
+    // epilogue: C[m][n] of block (mb, nb): m = 16 mb + 4 bj + i, n = 64 wave + 16 nb + bn
+    const int ks = max(1, g.ksplit);
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int n = n0 + 16 * NB * wave + 16 * nb + bn;
         if (n >= n_rows) continue;
         const float bias = sg.bias && z == 0 ? sg.bias[n] : 0.f;
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int m = m0 + 16 * mb + 4 * (lane >> 4) + i;
+                const int m = m0 + 16 * mb + 4 * bj + i;
                 if (m >= g.m) continue;
-                const float v = (i == 0 ? acc[mb][nb].x : i == 1 ? acc[mb][nb].y : i == 2 ? acc[mb][nb].z : acc[mb][nb].w) + bias;
+                const float v = acc[mb][nb][i] + bias;
                 const size_t o = (size_t)m * g.ldy + sg.col0 + n;
                 if (ks > 1) g.part[(size_t)z * g.m * g.ldy + o] = v;
                 else if (g.mode == MV_ADD) g.y[o] = g.res[o] + v;
                 else g.y[o] = v;
             }
         }
+    }
+}
+
+template <int TA, int TB, int MT>
+__global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t plds[];   // X tiles [2][MT][kLdsRow]
+    int si = 0;
+    if (g.nseg > 1 && (int)blockIdx.x >= g.seg[1].tile0) si = 1;
+    if (g.nseg > 2 && (int)blockIdx.x >= g.seg[2].tile0) si = 2;
+    const PrefillSeg& sg = g.seg[si];
+    const int m0 = blockIdx.y * MT, n0 = ((int)blockIdx.x - sg.tile0) * kGemmTileN;
+    const int n_kt = (g.k + kTileK - 1) / kTileK;
+    const int ks = max(1, g.ksplit), z = blockIdx.z;
+    const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
+    if constexpr (TA == TB) {
+        gemm_tile<TA, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
+    } else {
+        if (si == 2) gemm_tile<TB, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
+        else gemm_tile<TA, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
     }
 }
 
@@ -707,16 +664,27 @@ hipError_t attention_dispatch_prefill(const PrefillRows& p, hipStream_t st) {
 int gemm_rows_tile(int m) { return m <= 32 ? 32 : kTileM; }
 
 int prefill_gemm_splits(int m, int k, int n_tiles) {
-    // enough workgroups for two per CU on 256 CUs, at least 4 K tiles per split, at most 8 splits
+    // The split count with the shortest makespan in K tiles: rounds of
+    // resident workgroups (two per CU on 256 CUs, four with 32-row tiles) times K tiles per
+    // split, at least 2 K tiles per split, at most 8 splits; ties go to fewer.
     const int mt = gemm_rows_tile(m);
     const int wgs = n_tiles * ((m + mt - 1) / mt);
     const int n_kt = (k + kTileK - 1) / kTileK;
-    int ks = 1;
-    while (ks < 8 && wgs * ks < 512 && n_kt / (2 * ks) >= 4) ks *= 2;
-    return ks;
+    const int slots = 256 * (mt == 32 ? 4 : 2);
+    int best = 1;
+    long best_t = -1;
+    for (int ks = 1; ks <= 8 && (ks == 1 || n_kt / ks >= 2); ks++) {
+        const long rounds = ((long)wgs * ks + slots - 1) / slots;
+        const long t = rounds * ((n_kt + ks - 1) / ks);
+        if (best_t < 0 || t < best_t) {
+            best_t = t;
+            best = ks;
+        }
+    }
+    return best;
 }
 
-size_t prefill_gemm_lds_bytes() { return (size_t)(kTileM + kTileN) * kLdsRow * 2; }
+size_t prefill_gemm_lds_bytes() { return (size_t)2 * kTileM * kLdsRow * 2; }
 
 hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     if (g.m <= 0 || g.k <= 0 || g.k % 32 || g.nseg < 1 || g.nseg > 3) return hipErrorInvalidValue;
@@ -727,7 +695,7 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
         if (w.k != (uint32_t)g.k || w.rows == 0 || (w.type != 8 && g.k % 256) || g.seg[i].tile0 != tiles)
             return hipErrorInvalidValue;
         if (i < 2 && w.type != g.seg[0].w.type) return hipErrorInvalidValue;
-        tiles += (int)((w.rows + kTileN - 1) / kTileN);
+        tiles += gemm_tiles((int)w.rows);
     }
     const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
     const int ks = g.part ? max(1, g.ksplit) : 1;
@@ -736,7 +704,7 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     const dim3 grid(tiles, (g.m + mt - 1) / mt, ks);
     PrefillGemm gg = g;
     gg.ksplit = ks;
-    const size_t lds = (size_t)(mt + kTileN) * kLdsRow * 2;
+    const size_t lds = (size_t)2 * mt * kLdsRow * 2;
 #define RIBN_PG(A, B)                                                                                           \
     if (ta == A && tb == B) {                                                                                   \
         hipError_t e;                                                                                           \
