@@ -157,7 +157,7 @@ def run_config3(args):
     prompts = [rng.integers(0, CFG["vocab"], int(n)).tolist() for n in rng.integers(256, 2049, n_seq)]
     try:
         with ribn_amd.QwenRocm(path, context_tokens=2048 + n_out + 16, max_sequences=n_seq,
-                               max_batch_tokens=budget) as m:
+                               max_batch_tokens=budget, kv="bf16") as m:
             seqs = {}
             for i, p in enumerate(prompts):
                 a = m.admit(1000 + i, i + 1, p, n_out)
@@ -213,7 +213,7 @@ def run_config3(args):
            "decode_phase_tok_s": round(decode_after / max(1e-9, t0 + wall - t_all_prefilled), 1)
            if t_all_prefilled else None,
            "median_first_token_s": round(float(np.median(first_token_s)), 2),
-           "config": {"workload": "BASELINE configs[3]", "sequences": n_seq, "prompt": "U[256,2048]",
+           "config": {"workload": "BASELINE configs[3]", "kv": "bf16 paged, 16-token pages", "sequences": n_seq, "prompt": "U[256,2048]",
                       "chunk": chunk, "batch_token_budget": budget, "decode_tokens": n_out},
            "note": "a batch's decode rows run as one batched step through the MFMA GEMMs (per-row split-K "
                    "attention over each sequence's pages); prefill rows run chunked MFMA prefill"}
@@ -267,7 +267,7 @@ def run_config4(args):
     prompt = np.random.default_rng(0).integers(0, cfg["vocab"], args.c4_prompt).tolist()
     try:
         with ribn_amd.QwenRocm(path, context_tokens=args.c4_prompt + 256 + 16, max_sequences=1,
-                               max_batch_tokens=2048) as m:
+                               max_batch_tokens=2048, kv="bf16") as m:
             info = m.info
             toks, tm = m.generate(prompt, 257)
     finally:
@@ -280,7 +280,7 @@ def run_config4(args):
            "ms_per_step": round(tm.decode_ms / 256, 3),
            "step_hbm": {"bytes_per_token": int(step_bytes),
                         "achieved_gbs": round(step_bytes / (tm.decode_ms / 256 / 1e3) / 1e9, 1)},
-           "config": {"workload": "BASELINE configs[4]", "prompt": args.c4_prompt, "prefill_chunk": 2048,
+           "config": {"workload": "BASELINE configs[4]", "kv": "bf16 paged, 16-token pages", "prompt": args.c4_prompt, "prefill_chunk": 2048,
                       "decode_tokens": 256, "layers": cfg["layers"]},
            "setup_s": {"synth": round(t_synth, 1)}}
     print(json.dumps(out))
