@@ -148,7 +148,7 @@ def test_chunked_prefill_hidden_and_logits(model_paths, name, kv, chunk):
 @pytest.mark.parametrize("step", STEPS)
 @pytest.mark.parametrize("kv", list(KV_MODES))
 def test_long_context_split_k(model_paths, kv, step):
-    """700 positions: 16 splits over 44 pages, log-sum-exp merge across workgroups."""
+    """700 positions: 8 splits of 96 over 44 pages, log-sum-exp merge across workgroups."""
     path = model_paths["qwen3_q4km_hd128_g4"]
     kv_round, tol = KV_MODES[kv]
     rng = np.random.default_rng(2)
@@ -160,6 +160,28 @@ def test_long_context_split_k(model_paths, kv, step):
     ref_l, _ = _oracle_trace(path, tokens, 1024, kv_round=kv_round)
     for lo in (0, 100, 300, 600):
         r = _rel(lg[lo:lo + 100], ref_l[lo:lo + 100])
+        assert r <= tol, (lo, r)
+
+
+@pytest.mark.parametrize("kv", list(KV_MODES))
+def test_split_policy_regimes(tmp_path, kv):
+    """8400 positions through every regime of the split policy: one workgroup up to 128 positions, then
+    splits of about 128 (up to 2048), 256 (up to 8192) and 1024 positions (flash-decoding blocks across a
+    whole 1024-position split); logits at each boundary and at the end against the FP32 oracle. One layer,
+    one KV head, Q8_0, so the oracle's quadratic attention stays within seconds."""
+    path = str(tmp_path / "long.gguf")
+    ribn_amd.synth_qwen_gguf(path, qwen3=False, hidden=128, layers=1, q_heads=2, kv_heads=1, head_dim=64, ffn=256,
+                             vocab=256, weight_type=ribn_amd.GGML_Q8_0, seed=7, norm_jitter=0.15, weight_std=0.05)
+    kv_round, tol = KV_MODES[kv]
+    n = 8400
+    tokens = np.random.default_rng(5).integers(0, 256, n).tolist()
+    say(f"trace {n} tokens kv={kv}")
+    with ribn_amd.QwenRocm(path, context_tokens=n + 16, max_sequences=1, kv=kv) as m:
+        _, lg, _ = m.trace(tokens, logits=True)
+    ref_l, _ = _oracle_trace(path, tokens, n + 16, kv_round=kv_round)
+    for lo, hi in ((0, 160), (2030, 2070), (8180, 8210), (n - 40, n)):
+        r = _rel(lg[lo:hi], ref_l[lo:hi])
+        say(f"  positions {lo}..{hi}: rel-L2 {r:.2e}")
         assert r <= tol, (lo, r)
 
 
