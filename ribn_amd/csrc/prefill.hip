@@ -304,14 +304,18 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     }
 }
 
-// y = (res) + sum over z of part[z] (fixed order: deterministic)
+// y = (res) + part[0] + ... + part[ks - 1], in split order (deterministic).
+// Four values per thread; n is a multiple of 4.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int ks, size_t n, const float* res,
-                                                            float* y, int add) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+                                                            float* y) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
-    float v = add ? res[i] : 0.f;
-    for (int z = 0; z < ks; z++) v += part[(size_t)z * n + i];
-    y[i] = v;
+    float4 v = res ? *reinterpret_cast<const float4*>(res + i) : float4{0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < ks; z++) {
+        const float4 p = *reinterpret_cast<const float4*>(part + (size_t)z * n + i);
+        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    *reinterpret_cast<float4*>(y + i) = v;
 }
 
 // rows x[m][k] -> f16(rms_norm(x) * w) (rms_norm, model_ops.rs:108-157); w may be null
@@ -698,7 +702,10 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
         tiles += gemm_tiles((int)w.rows);
     }
     const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
-    const int ks = g.part ? max(1, g.ksplit) : 1;
+    // split-K needs the partial workspace and whole float4s of y for the reduction
+    const bool can_split = g.part && ((size_t)g.m * g.ldy) % 4 == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15) == 0 &&
+                           (reinterpret_cast<uintptr_t>(g.res) & 15) == 0;
+    const int ks = can_split ? max(1, g.ksplit) : 1;
     if (ks > 1 && ks > (g.k + kTileK - 1) / kTileK) return hipErrorInvalidValue;
     const int mt = gemm_rows_tile(g.m);
     const dim3 grid(tiles, (g.m + mt - 1) / mt, ks);
@@ -722,8 +729,8 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
         e = hipGetLastError();                                                                                  \
         if (e != hipSuccess || ks == 1) return e;                                                               \
         const size_t n = (size_t)g.m * g.ldy;                                                                   \
-        splitk_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(g.part, ks, n, g.res, g.y,            \
-                                                                          g.mode == MV_ADD ? 1 : 0);            \
+        splitk_reduce_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(g.part, ks, n,                    \
+                                                                               g.mode == MV_ADD ? g.res : nullptr, g.y); \
         return hipGetLastError();                                                                               \
     }
     RIBN_PG(12, 12) RIBN_PG(14, 14) RIBN_PG(8, 8) RIBN_PG(12, 14) RIBN_PG(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
