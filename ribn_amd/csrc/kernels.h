@@ -190,7 +190,17 @@ struct PrefillGemm {
     // reduction then writes y = (res) + sum of the partials
     int ksplit;
     float* part;
+    // optional step fused after the result (into the split-K reduction when
+    // there is one, else a separate launch), per output row r:
+    //   GEMM_POST_RMS_F16:  post_out[r][i] = f16(rms_norm(y[r]) * post_w[i]), y written too
+    //   GEMM_POST_SILU_F16: y[r] = gate | up halves of ldy / 2 columns;
+    //                       post_out[r][j] = f16(silu(gate) * up), y not written when split
+    int post;
+    const float* post_w;
+    float post_eps;
+    uint16_t* post_out;
 };
+constexpr int GEMM_POST_NONE = 0, GEMM_POST_RMS_F16 = 1, GEMM_POST_SILU_F16 = 2;
 
 // Rows of one prefill chunk at positions pos0 .. pos0 + m - 1.
 struct PrefillRows {

@@ -625,9 +625,11 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     rows.eps = M->eps;
     rows.pages = M->d_pages + (size_t)slot * M->max_pages;
     // one launch per input: q|k|v, attn_output, gate|up, down
-    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs) {
+    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
+                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr) {
         PrefillGemm g{};
         g.x = x; g.m = m; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
+        g.post = post; g.post_w = post_w; g.post_eps = M->eps; g.post_out = post_out;
         int tiles = 0;
         for (const PrefillSeg& sg : segs) {
             g.seg[g.nseg] = sg;
@@ -642,7 +644,10 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     };
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
-        if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        // layer l > 0 receives its normed input from the previous down GEMM
+        if (l == 0 &&
+            (e = launch_rows_rms_f16(M->p_h, m, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess)
+            return e;
         if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
                       {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
                        PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
@@ -653,13 +658,18 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
         rows.vcache = y.vc;
         if ((e = launch_qk_rope_append(rows, st)) != hipSuccess) return e;
         if ((e = launch_prefill_attention(rows, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}})) != hipSuccess) return e;
-        if ((e = launch_rows_rms_f16(M->p_h, m, M->H, y.ffn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
-                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}})) != hipSuccess)
+        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
+                      y.ffn_norm, M->p_x16)) != hipSuccess)
             return e;
-        if ((e = launch_silu_mul_f16(M->p_gu, M->F, m, M->p_act16, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}})) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
+                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}}, GEMM_POST_SILU_F16, nullptr,
+                      M->p_act16)) != hipSuccess)
+            return e;
+        const bool more = l + 1 < M->L;
+        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}},
+                      more ? GEMM_POST_RMS_F16 : GEMM_POST_NONE, more ? M->layers[l + 1].attn_norm : nullptr,
+                      M->p_x16)) != hipSuccess)
+            return e;
         if ((e = snap(l + 1)) != hipSuccess) return e;
     }
     SeqState* seq = &M->d_slots[slot];
@@ -707,9 +717,11 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     if ((e = launch_gather_row_tokens(M->d_tokens, M->context + 1, dr, M->d_btokens, st)) != hipSuccess) return e;
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
-    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs) {
+    auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
+                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr) {
         PrefillGemm g{};
         g.x = x; g.m = n; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
+        g.post = post; g.post_w = post_w; g.post_eps = M->eps; g.post_out = post_out;
         int tiles = 0;
         for (const PrefillSeg& sg : segs) {
             g.seg[g.nseg] = sg;
@@ -725,7 +737,10 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
-        if ((e = launch_rows_rms_f16(M->p_h, n, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
+        // layer l > 0 receives its normed input from the previous down GEMM
+        if (l == 0 &&
+            (e = launch_rows_rms_f16(M->p_h, n, M->H, y.attn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess)
+            return e;
         if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
                       {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
                        PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
@@ -733,15 +748,19 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
         AttnArgs at = attn_args(M, l, n_splits);
         if ((e = launch_attention_rows(at, dr, st)) != hipSuccess) return e;
         if ((e = launch_rows_rms_f16(M->b_att, n, qd, nullptr, 0.f, false, M->p_att16, qd, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}})) != hipSuccess) return e;
-        if ((e = launch_rows_rms_f16(M->p_h, n, M->H, y.ffn_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
-                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}})) != hipSuccess)
+        if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
+                      y.ffn_norm, M->p_x16)) != hipSuccess)
             return e;
-        if ((e = launch_silu_mul_f16(M->p_gu, M->F, n, M->p_act16, st)) != hipSuccess) return e;
-        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}})) != hipSuccess) return e;
+        if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
+                      {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}}, GEMM_POST_SILU_F16, nullptr,
+                      M->p_act16)) != hipSuccess)
+            return e;
+        // the last layer's down GEMM norms the rows for the head
+        const float* next_norm = l + 1 < M->L ? M->layers[l + 1].attn_norm : M->out_norm;
+        if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
+                      next_norm, M->p_x16)) != hipSuccess)
+            return e;
     }
-    if ((e = launch_rows_rms_f16(M->p_h, n, M->H, M->out_norm, M->eps, true, M->p_x16, M->H, st)) != hipSuccess) return e;
     if ((e = gemm(M->p_x16, M->H, M->b_logits, M->V, MV_STORE, {PrefillSeg{M->out, 0, 0, nullptr}})) != hipSuccess)
         return e;
     return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);

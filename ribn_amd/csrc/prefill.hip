@@ -318,6 +318,68 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
     *reinterpret_cast<float4*>(y + i) = v;
 }
 
+// Split-K reduction with the RMSNorm of the next GEMM's input fused: one
+// workgroup per row r: y[r] = (res[r]) + part[0][r] + ... (split order), then
+// out[r][i] = f16(y[r][i] * inv * w[i]), inv = 1/sqrt(sum(y^2)/n + eps)
+// (rms_norm, model_ops.rs:108-157). n is a multiple of 4 and at most 8192.
+__global__ __launch_bounds__(256) void splitk_reduce_rms_kernel(const float* part, int ks, int m, int n, const float* res,
+                                                                float* y, const float* w, float eps, uint16_t* out) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const size_t plane = (size_t)m * n, row = (size_t)r * n;
+    float4 v[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = 4 * tid + 1024 * j;
+        if (i < n) {
+            float4 a = res ? *reinterpret_cast<const float4*>(res + row + i) : float4{0.f, 0.f, 0.f, 0.f};
+            for (int z = 0; z < ks; z++) {
+                const float4 p = *reinterpret_cast<const float4*>(part + z * plane + row + i);
+                a.x += p.x; a.y += p.y; a.z += p.z; a.w += p.w;
+            }
+            *reinterpret_cast<float4*>(y + row + i) = a;
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+            v[j] = a;
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = 4 * tid + 1024 * j;
+        if (i < n) {
+            const float4 wv = *reinterpret_cast<const float4*>(w + i);
+            *reinterpret_cast<uint2*>(out + row + i) =
+                uint2{pack_h2(v[j].x * inv * wv.x, v[j].y * inv * wv.y), pack_h2(v[j].z * inv * wv.z, v[j].w * inv * wv.w)};
+        }
+    }
+}
+
+// Split-K reduction of a gate | up GEMM with SwiGLU fused (silu_mul,
+// model_ops.rs:318-330): act[r][j] = f16(g / (1 + exp(-g)) * u) for the summed
+// g = y[r][j], u = y[r][f + j] (split order); the sums themselves are not
+// stored. Four columns per thread; f is a multiple of 4.
+__global__ __launch_bounds__(256) void splitk_reduce_silu_kernel(const float* part, int ks, int m, int f, uint16_t* act) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per_row = (size_t)f / 4;
+    if (t >= (size_t)m * per_row) return;
+    const size_t r = t / per_row, j = (t % per_row) * 4;
+    const size_t plane = (size_t)m * 2 * f, gi = r * 2 * f + j, ui = gi + f;
+    float4 g{0.f, 0.f, 0.f, 0.f}, u{0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < ks; z++) {
+        const float4 pg = *reinterpret_cast<const float4*>(part + z * plane + gi);
+        const float4 pu = *reinterpret_cast<const float4*>(part + z * plane + ui);
+        g.x += pg.x; g.y += pg.y; g.z += pg.z; g.w += pg.w;
+        u.x += pu.x; u.y += pu.y; u.z += pu.z; u.w += pu.w;
+    }
+    auto sw = [](float a, float b) { return a / (1.0f + expf(-a)) * b; };
+    *reinterpret_cast<uint2*>(act + r * f + j) = uint2{pack_h2(sw(g.x, u.x), sw(g.y, u.y)), pack_h2(sw(g.z, u.z), sw(g.w, u.w))};
+}
+
 // rows x[m][k] -> f16(rms_norm(x) * w) (rms_norm, model_ops.rs:108-157); w may be null
 // (plain conversion). One workgroup per row.
 __global__ __launch_bounds__(256) void rows_rms_f16_kernel(const float* x, int k, const float* w, float eps, int norm,
@@ -690,6 +752,30 @@ int prefill_gemm_splits(int m, int k, int n_tiles) {
 
 size_t prefill_gemm_lds_bytes() { return (size_t)2 * kTileM * kLdsRow * 2; }
 
+// After the GEMM: the split-K reduction (with the fused step, if any), or the
+// fused step on its own for an unsplit GEMM.
+static hipError_t gemm_post(const PrefillGemm& g, int ks, hipStream_t st) {
+    const float* res = g.mode == MV_ADD ? g.res : nullptr;
+    if (ks == 1) {
+        if (g.post == GEMM_POST_RMS_F16) return launch_rows_rms_f16(g.y, g.m, g.ldy, g.post_w, g.post_eps, true, g.post_out, g.ldy, st);
+        if (g.post == GEMM_POST_SILU_F16) return launch_silu_mul_f16(g.y, g.ldy / 2, g.m, g.post_out, st);
+        return hipSuccess;
+    }
+    if (g.post == GEMM_POST_RMS_F16) {
+        splitk_reduce_rms_kernel<<<(unsigned)g.m, 256, 0, st>>>(g.part, ks, g.m, g.ldy, res, g.y, g.post_w, g.post_eps,
+                                                                 g.post_out);
+        return hipGetLastError();
+    }
+    if (g.post == GEMM_POST_SILU_F16) {
+        const size_t t = (size_t)g.m * (g.ldy / 2) / 4;
+        splitk_reduce_silu_kernel<<<(unsigned)((t + 255) / 256), 256, 0, st>>>(g.part, ks, g.m, g.ldy / 2, g.post_out);
+        return hipGetLastError();
+    }
+    const size_t n = (size_t)g.m * g.ldy;
+    splitk_reduce_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(g.part, ks, n, res, g.y);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     if (g.m <= 0 || g.k <= 0 || g.k % 32 || g.nseg < 1 || g.nseg > 3) return hipErrorInvalidValue;
     int tiles = 0;
@@ -703,6 +789,8 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     }
     const uint32_t ta = g.seg[0].w.type, tb = g.seg[g.nseg - 1].w.type;
     // split-K needs the partial workspace and whole float4s of y for the reduction
+    if (g.post == GEMM_POST_RMS_F16 && (!g.post_w || !g.post_out || g.ldy > 8192)) return hipErrorInvalidValue;
+    if (g.post == GEMM_POST_SILU_F16 && (!g.post_out || g.mode != MV_STORE || g.ldy % 8)) return hipErrorInvalidValue;
     const bool can_split = g.part && ((size_t)g.m * g.ldy) % 4 == 0 && (reinterpret_cast<uintptr_t>(g.y) & 15) == 0 &&
                            (reinterpret_cast<uintptr_t>(g.res) & 15) == 0;
     const int ks = can_split ? max(1, g.ksplit) : 1;
@@ -727,11 +815,8 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
             prefill_gemm_kernel<A, B, kTileM><<<grid, kGemmThreads, lds, st>>>(gg);                             \
         }                                                                                                       \
         e = hipGetLastError();                                                                                  \
-        if (e != hipSuccess || ks == 1) return e;                                                               \
-        const size_t n = (size_t)g.m * g.ldy;                                                                   \
-        splitk_reduce_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, st>>>(g.part, ks, n,                    \
-                                                                               g.mode == MV_ADD ? g.res : nullptr, g.y); \
-        return hipGetLastError();                                                                               \
+        if (e != hipSuccess) return e;                                                                          \
+        return gemm_post(g, ks, st);                                                                            \
     }
     RIBN_PG(12, 12) RIBN_PG(14, 14) RIBN_PG(8, 8) RIBN_PG(12, 14) RIBN_PG(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
     RIBN_PG(14, 8) RIBN_PG(8, 14)
