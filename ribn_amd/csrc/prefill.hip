@@ -520,10 +520,14 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(PrefillRows p) {
 // A binary16 cache is used as stored; a bfloat16 cache is converted to binary16
 // when staged (exact for values in binary16's normal range).
 constexpr int kAttKeys = 32;
+// 16-row blocks per workgroup: about four (row block, head) tiles, one per wave
+// (8 or 16 tiles per workgroup measured slower: one workgroup per CU)
+template <int G>
+__host__ __device__ constexpr int att_row_blocks() { return G >= 4 ? 1 : 4 / G; }
 
 template <int HD, int G, bool F16KV>
 __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
-    constexpr int RB = G >= 4 ? 1 : 4 / G;     // 16-row blocks per workgroup
+    constexpr int RB = att_row_blocks<G>();     // 16-row blocks per workgroup
     constexpr int NT = RB * G;                  // tiles
     constexpr int TPW = (NT + 3) / 4;           // tiles per wave
     constexpr int NC = HD / 32;                 // 32-dim chunks of q.k
@@ -703,7 +707,7 @@ __global__ void set_pos_kernel(SeqState* s, int pos) {
 
 template <int HD, int G>
 hipError_t attention_launch_prefill(const PrefillRows& p, hipStream_t st) {
-    constexpr int RB = G >= 4 ? 1 : 4 / G;
+    constexpr int RB = att_row_blocks<G>();
     const dim3 grid((p.m + 16 * RB - 1) / (16 * RB), p.hkv);
     if (p.kv_f16) prefill_attention_kernel<HD, G, true><<<grid, 256, 0, st>>>(p);
     else prefill_attention_kernel<HD, G, false><<<grid, 256, 0, st>>>(p);
