@@ -65,6 +65,12 @@ typedef struct {
  * stages) when one is compiled for the model's configuration, instead of the
  * default chain of per-stage launches replayed as HIP graphs. */
 #define RIBN_LOAD_PERSISTENT_STEP 2u
+/* Keep a binary16 copy of every layer matrix and of the output head, dequantized
+ * once at load (exactly, then rounded to binary16), and run chunked prefill and
+ * batched decode as plain hipBLASLt GEMMs on it instead of the dequantizing MFMA
+ * GEMM. Costs 2 bytes per weight of extra HBM (16.4 GB for an 8B model); the
+ * batch-1 decode matvecs keep streaming the GGUF planes. */
+#define RIBN_LOAD_RESIDENT_F16 4u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);

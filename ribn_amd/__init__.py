@@ -33,6 +33,7 @@ BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q8_0: (32, 34), GGML_Q4_K: (25
 RIBN_OK, RIBN_PENDING = 0, 1
 LOAD_KV_BF16 = 1
 LOAD_PERSISTENT_STEP = 2
+LOAD_RESIDENT_F16 = 4
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -279,13 +280,18 @@ class QwenRocm:
     """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
-                 kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain"):
+                 kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain", gemm: str = "dequant"):
         """step: "persistent" (one kernel launch per token step when the library has a kernel compiled for
-        this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs)."""
+        this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs).
+        gemm: "dequant" (chunked prefill and batched decode on the dequantizing MFMA GEMM) or "resident"
+        (binary16 copies of the weights made at load, hipBLASLt GEMMs)."""
+        if gemm not in ("dequant", "resident"):
+            raise ValueError("gemm must be 'dequant' or 'resident'")
         if step not in ("persistent", "chain"):
             raise ValueError("step must be 'persistent' or 'chain'")
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
-                           (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0))
+                           (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0)
+                           | (LOAD_RESIDENT_F16 if gemm == "resident" else 0))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()

@@ -280,6 +280,15 @@ hipError_t launch_rows_argmax_commit(const float* logits, int V, const DecodeRow
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t stream);
 hipError_t launch_dequant(const QMat& w, float* out, hipStream_t stream);
+hipError_t launch_dequant_f16(const QMat& w, uint16_t* out, hipStream_t stream);
+
+// Plain binary16 GEMM on hipBLASLt for resident dequantized weights:
+// y[m][ldy] (+)= x[m][k] w16[n][k]^T (+ bias[n]), FP32 output and accumulation.
+struct BlasGemm;
+hipError_t blas_create(BlasGemm** out, hipStream_t stream);
+void blas_destroy(BlasGemm* b);
+hipError_t blas_gemm(BlasGemm* b, const uint16_t* x, int m, int k, const uint16_t* w16, int n, float* y, int ldy,
+                     bool add, const float* bias, hipStream_t stream);
 // A compiled configuration of the persistent step kernel: matrix value types
 // (q/k, v, attn_output, gate/up, down, head), head dimension, query heads per
 // KV head, KV element type.

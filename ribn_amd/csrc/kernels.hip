@@ -29,6 +29,16 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(QMat w, float* out) {
     out[idx] = deq_elem(w, (uint32_t)(idx / w.k), (uint32_t)(idx % w.k));
 }
 
+// Rows of w dequantized exactly and rounded to binary16 (RNE): out[r][e] for
+// r < w.rows, row stride w.k (the resident-weight GEMM operands).
+__global__ __launch_bounds__(kThreads) void dequant_f16_kernel(QMat w, uint16_t* out) {
+    const size_t idx = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    const size_t total = (size_t)w.rows * w.k;
+    if (idx >= total) return;
+    const float v = deq_elem(w, (uint32_t)(idx / w.k), (uint32_t)(idx % w.k));
+    out[idx] = __half_as_ushort(__float2half_rn(v));
+}
+
 // Token embedding: one row of token_embd dequantized exactly
 // (q4_k_embedding, kernels/quantized/q4_k.cu:1; reference decode.rs:577-582),
 // plus the step's rotary table: theta_p = pos * base^(-2p/rot) in f32 and its
@@ -308,6 +318,13 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t st) {
 
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t st) {
     advance_kernel<<<1, 64, 0, st>>>(ctl);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_f16(const QMat& w, uint16_t* out, hipStream_t st) {
+    const size_t total = (size_t)w.rows * w.k;
+    if (total == 0) return hipSuccess;
+    dequant_f16_kernel<<<(unsigned)((total + kThreads - 1) / kThreads), kThreads, 0, st>>>(w, out);
     return hipGetLastError();
 }
 

@@ -33,6 +33,10 @@ struct Layer {
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     float *q_bias = nullptr, *k_bias = nullptr, *v_bias = nullptr;
     uint16_t *kc = nullptr, *vc = nullptr;
+    // resident binary16 weights (RIBN_LOAD_RESIDENT_F16): q|k|v and gate|up
+    // concatenated by output row, with the q|k|v bias concatenated likewise
+    uint16_t *w16_qkv = nullptr, *w16_o = nullptr, *w16_gu = nullptr, *w16_down = nullptr;
+    float* qkv_bias = nullptr;
 };
 
 struct Sequence {
@@ -74,6 +78,8 @@ struct ribn_rocm_model {
     uint64_t weight_bytes = 0, kv_bytes = 0;
 
     QMat embd{}, out{};
+    uint16_t* w16_head = nullptr;   // resident binary16 output head
+    BlasGemm* blas = nullptr;       // hipBLASLt state when the weights are resident
     float* out_norm = nullptr;
     std::vector<Layer> layers;
 
@@ -594,6 +600,20 @@ hipError_t graph_step(ribn_rocm_model* M, bool head, int ctx) {
     return hipGraphLaunch(it->second, M->stream);
 }
 
+// A prefill / batched-decode projection: the dequantizing MFMA GEMM, or with
+// resident binary16 weights (w16, n output rows, optional concatenated bias) a
+// hipBLASLt GEMM followed by the fused step as its own launch.
+hipError_t run_gemm(ribn_rocm_model* M, const PrefillGemm& g, const uint16_t* w16, int n, const float* bias,
+                    hipStream_t st) {
+    if (!M->blas || !w16) return launch_prefill_gemm(g, st);
+    hipError_t e = blas_gemm(M->blas, g.x, g.m, g.k, w16, n, g.y, g.ldy, g.mode == MV_ADD, bias, st);
+    if (e != hipSuccess) return e;
+    if (g.post == GEMM_POST_RMS_F16)
+        return launch_rows_rms_f16(g.y, g.m, g.ldy, g.post_w, g.post_eps, true, g.post_out, g.ldy, st);
+    if (g.post == GEMM_POST_SILU_F16) return launch_silu_mul_f16(g.y, g.ldy / 2, g.m, g.post_out, st);
+    return hipSuccess;
+}
+
 // One prefill chunk of the sequence in `slot`: rows pos0 .. pos0 + m - 1 of its
 // token array through every layer (prefill_chunk, nvidia/src/decode.rs:2124).
 // final: the last row's hidden state goes through the head and its greedy
@@ -626,7 +646,8 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     rows.pages = M->d_pages + (size_t)slot * M->max_pages;
     // one launch per input: q|k|v, attn_output, gate|up, down
     auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
-                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr) {
+                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr,
+                    const uint16_t* w16 = nullptr, const float* bias16 = nullptr) {
         PrefillGemm g{};
         g.x = x; g.m = m; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
         g.post = post; g.post_w = post_w; g.post_eps = M->eps; g.post_out = post_out;
@@ -640,7 +661,7 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
         g.ksplit = prefill_gemm_splits(m, k, tiles);
         if (g.ksplit > 1 && (size_t)g.ksplit * m * ldy <= M->p_part_floats) g.part = M->p_part;
         else g.ksplit = 1;
-        return launch_prefill_gemm(g, st);
+        return run_gemm(M, g, w16, ldy, bias16, st);
     };
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
@@ -650,7 +671,8 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
             return e;
         if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
                       {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
-                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
+                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}},
+                      GEMM_POST_NONE, nullptr, nullptr, y.w16_qkv, y.qkv_bias)) != hipSuccess)
             return e;
         rows.q_norm = y.q_norm;
         rows.k_norm = y.k_norm;
@@ -659,16 +681,16 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
         if ((e = launch_qk_rope_append(rows, st)) != hipSuccess) return e;
         if ((e = launch_prefill_attention(rows, st)) != hipSuccess) return e;
         if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
-                      y.ffn_norm, M->p_x16)) != hipSuccess)
+                      y.ffn_norm, M->p_x16, y.w16_o)) != hipSuccess)
             return e;
         if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
                       {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}}, GEMM_POST_SILU_F16, nullptr,
-                      M->p_act16)) != hipSuccess)
+                      M->p_act16, y.w16_gu)) != hipSuccess)
             return e;
         const bool more = l + 1 < M->L;
         if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}},
                       more ? GEMM_POST_RMS_F16 : GEMM_POST_NONE, more ? M->layers[l + 1].attn_norm : nullptr,
-                      M->p_x16)) != hipSuccess)
+                      M->p_x16, y.w16_down)) != hipSuccess)
             return e;
         if ((e = snap(l + 1)) != hipSuccess) return e;
     }
@@ -720,7 +742,8 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
     auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
-                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr) {
+                    int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr,
+                    const uint16_t* w16 = nullptr, const float* bias16 = nullptr) {
         PrefillGemm g{};
         g.x = x; g.m = n; g.k = k; g.y = y; g.ldy = ldy; g.res = y; g.mode = mode;
         g.post = post; g.post_w = post_w; g.post_eps = M->eps; g.post_out = post_out;
@@ -734,7 +757,7 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
         g.ksplit = prefill_gemm_splits(n, k, tiles);
         if (g.ksplit > 1 && (size_t)g.ksplit * n * ldy <= M->p_part_floats) g.part = M->p_part;
         else g.ksplit = 1;
-        return launch_prefill_gemm(g, st);
+        return run_gemm(M, g, w16, ldy, bias16, st);
     };
     const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
     for (int l = 0; l < M->L; l++) {
@@ -745,25 +768,27 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
             return e;
         if ((e = gemm(M->p_x16, M->H, M->p_qkv, ldq, MV_STORE,
                       {PrefillSeg{y.q, 0, 0, y.q_bias}, PrefillSeg{y.k, qd, 0, y.k_bias},
-                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}})) != hipSuccess)
+                       PrefillSeg{y.v, qd + kd, 0, y.v_bias}},
+                      GEMM_POST_NONE, nullptr, nullptr, y.w16_qkv, y.qkv_bias)) != hipSuccess)
             return e;
         AttnArgs at = attn_args(M, l, n_splits);
         if ((e = launch_attention_rows(at, dr, st)) != hipSuccess) return e;
         if ((e = launch_rows_rms_f16(M->b_att, n, qd, nullptr, 0.f, false, M->p_att16, qd, st)) != hipSuccess) return e;
         if ((e = gemm(M->p_att16, qd, M->p_h, M->H, MV_ADD, {PrefillSeg{y.o, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
-                      y.ffn_norm, M->p_x16)) != hipSuccess)
+                      y.ffn_norm, M->p_x16, y.w16_o)) != hipSuccess)
             return e;
         if ((e = gemm(M->p_x16, M->H, M->p_gu, 2 * M->F, MV_STORE,
                       {PrefillSeg{y.gate, 0, 0, nullptr}, PrefillSeg{y.up, M->F, 0, nullptr}}, GEMM_POST_SILU_F16, nullptr,
-                      M->p_act16)) != hipSuccess)
+                      M->p_act16, y.w16_gu)) != hipSuccess)
             return e;
         // the last layer's down GEMM norms the rows for the head
         const float* next_norm = l + 1 < M->L ? M->layers[l + 1].attn_norm : M->out_norm;
         if ((e = gemm(M->p_act16, M->F, M->p_h, M->H, MV_ADD, {PrefillSeg{y.down, 0, 0, nullptr}}, GEMM_POST_RMS_F16,
-                      next_norm, M->p_x16)) != hipSuccess)
+                      next_norm, M->p_x16, y.w16_down)) != hipSuccess)
             return e;
     }
-    if ((e = gemm(M->p_x16, M->H, M->b_logits, M->V, MV_STORE, {PrefillSeg{M->out, 0, 0, nullptr}})) != hipSuccess)
+    if ((e = gemm(M->p_x16, M->H, M->b_logits, M->V, MV_STORE, {PrefillSeg{M->out, 0, 0, nullptr}}, GEMM_POST_NONE,
+                  nullptr, nullptr, M->w16_head)) != hipSuccess)
         return e;
     return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);
 }
@@ -843,6 +868,43 @@ bool take_pages(ribn_rocm_model* M, uint32_t tokens, std::vector<int32_t>* out) 
 void give_pages(ribn_rocm_model* M, std::vector<int32_t>& pages) {
     M->free_pages.insert(M->free_pages.end(), pages.begin(), pages.end());
     pages.clear();
+}
+
+// RIBN_LOAD_RESIDENT_F16: binary16 copies of every layer matrix and the head,
+// and the hipBLASLt state that multiplies with them.
+hipError_t make_resident(ribn_rocm_model* M) {
+    hipStream_t st = M->stream;
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    auto copy = [&](uint16_t* dst, const QMat& w) { return launch_dequant_f16(w, dst, st); };
+    for (Layer& y : M->layers) {
+        hipError_t e;
+        if ((e = dalloc(M, &y.w16_qkv, 2ull * (qd + 2 * kd) * M->H)) != hipSuccess) return e;
+        if ((e = dalloc(M, &y.w16_o, 2ull * M->H * qd)) != hipSuccess) return e;
+        if ((e = dalloc(M, &y.w16_gu, 2ull * 2 * M->F * M->H)) != hipSuccess) return e;
+        if ((e = dalloc(M, &y.w16_down, 2ull * M->H * M->F)) != hipSuccess) return e;
+        if ((e = copy(y.w16_qkv, y.q)) != hipSuccess) return e;
+        if ((e = copy(y.w16_qkv + (size_t)qd * M->H, y.k)) != hipSuccess) return e;
+        if ((e = copy(y.w16_qkv + (size_t)(qd + kd) * M->H, y.v)) != hipSuccess) return e;
+        if ((e = copy(y.w16_o, y.o)) != hipSuccess) return e;
+        if ((e = copy(y.w16_gu, y.gate)) != hipSuccess) return e;
+        if ((e = copy(y.w16_gu + (size_t)M->F * M->H, y.up)) != hipSuccess) return e;
+        if ((e = copy(y.w16_down, y.down)) != hipSuccess) return e;
+        if (y.q_bias) {
+            if ((e = dalloc(M, &y.qkv_bias, sizeof(float) * (qd + 2 * kd))) != hipSuccess) return e;
+            const float* parts[3] = {y.q_bias, y.k_bias, y.v_bias};
+            const int off[3] = {0, qd, qd + kd}, len[3] = {qd, kd, kd};
+            for (int i = 0; i < 3; i++) {
+                if (parts[i]) e = hipMemcpyAsync(y.qkv_bias + off[i], parts[i], sizeof(float) * len[i], hipMemcpyDeviceToDevice, st);
+                else e = hipMemsetAsync(y.qkv_bias + off[i], 0, sizeof(float) * len[i], st);
+                if (e != hipSuccess) return e;
+            }
+        }
+    }
+    hipError_t e = dalloc(M, &M->w16_head, 2ull * M->V * M->H);
+    if (e == hipSuccess) e = copy(M->w16_head, M->out);
+    if (e == hipSuccess) e = blas_create(&M->blas, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e;
 }
 
 std::string validate_type(const GgufTensor* t, const char* what, bool matrix) {
@@ -1105,6 +1167,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
     build_launches(M);
     HIPCHK(build_step(M, (o.flags & RIBN_LOAD_PERSISTENT_STEP) != 0));
+    if (o.flags & RIBN_LOAD_RESIDENT_F16) HIPCHK(make_resident(M));
     *out = Mp.release();
     return RIBN_OK;
 }
@@ -1114,6 +1177,7 @@ extern "C" void ribn_rocm_free(ribn_rocm_model* M) {
     if (M->stream) hipStreamSynchronize(M->stream);
     for (auto& kv : M->graphs) hipGraphExecDestroy(kv.second);
     if (M->pending.done) hipEventDestroy(M->pending.done);
+    blas_destroy(M->blas);
     for (void* p : M->dev_allocs) hipFree(p);
     for (void* p : M->host_allocs) hipHostFree(p);
     if (M->stream) hipStreamDestroy(M->stream);

@@ -122,19 +122,21 @@ def test_trace_hidden_and_logits(model_paths, name, kv, step):
         assert am[p] == orc.argmax(lg[p])   # the device argmax is the argmax of the device logits
 
 
+@pytest.mark.parametrize("gemm", ["dequant", "resident"])
 @pytest.mark.parametrize("chunk", [0, 16])
 @pytest.mark.parametrize("kv", list(KV_MODES))
 @pytest.mark.parametrize("name", list(MODELS))
-def test_chunked_prefill_hidden_and_logits(model_paths, name, kv, chunk):
+def test_chunked_prefill_hidden_and_logits(model_paths, name, kv, chunk, gemm):
     """Chunked prefill (MFMA GEMMs, causal chunk attention) against the FP32 oracle: hidden rows after every
     layer and the logits of every row; chunk 16 splits the 40 rows over three chunks, so later chunks attend
-    to cache entries written by earlier ones."""
+    to cache entries written by earlier ones. gemm "resident": the same projections as hipBLASLt GEMMs on
+    binary16 weight copies made at load."""
     path = model_paths[name]
     kv_round, tol = KV_MODES[kv]
     rng = np.random.default_rng(4)
     tokens = rng.integers(0, MODELS[name]["vocab"], 40).tolist()
     say(f"prefill trace {name} kv={kv} chunk={chunk}")
-    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=2, kv=kv) as m:
+    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=2, kv=kv, gemm=gemm) as m:
         lg, hd = m.prefill_trace(tokens, chunk=chunk, logits=True, hidden=True)
     ref_l, ref_h = _oracle_trace(path, tokens, 128, hidden=True, kv_round=kv_round)
     for layer in range(ref_h.shape[1]):
@@ -305,15 +307,16 @@ def test_executor_matches_generate(model_paths):
         m.synchronize()
 
 
+@pytest.mark.parametrize("gemm", ["dequant", "resident"])
 @pytest.mark.parametrize("name", ["qwen3_q4km_hd128_g4", "qwen2_q8_0_g7", "qwen3_g8_tied"])
-def test_batched_decode_rows_match_oracle(model_paths, name):
+def test_batched_decode_rows_match_oracle(model_paths, name, gemm):
     """Five sequences decoding together: every batch's decode rows run as one batched step (per-row
     positions and page tables, split-K attention per row, GEMM head, per-row argmax)."""
     path = model_paths[name]
     rng = np.random.default_rng(6)
     prompts = [rng.integers(0, MODELS[name]["vocab"], n).tolist() for n in (5, 17, 9, 33, 2)]
     say(f"batched decode {name}")
-    with ribn_amd.QwenRocm(path, context_tokens=64, max_sequences=5, max_batch_tokens=64) as m:
+    with ribn_amd.QwenRocm(path, context_tokens=64, max_sequences=5, max_batch_tokens=64, gemm=gemm) as m:
         outs = _run_engine(m, prompts, 12)
     for p, o in zip(prompts, outs):
         ref, ref_logits = _oracle_greedy(path, p, 12, 64, KV_MODES["f16"][0])
