@@ -157,7 +157,7 @@ def run_config3(args):
     prompts = [rng.integers(0, CFG["vocab"], int(n)).tolist() for n in rng.integers(256, 2049, n_seq)]
     try:
         with ribn_amd.QwenRocm(path, context_tokens=2048 + n_out + 16, max_sequences=n_seq,
-                               max_batch_tokens=budget, kv="bf16") as m:
+                               max_batch_tokens=budget, kv="bf16", gemm=args.gemm) as m:
             seqs = {}
             for i, p in enumerate(prompts):
                 a = m.admit(1000 + i, i + 1, p, n_out)
@@ -213,7 +213,7 @@ def run_config3(args):
            "decode_phase_tok_s": round(decode_after / max(1e-9, t0 + wall - t_all_prefilled), 1)
            if t_all_prefilled else None,
            "median_first_token_s": round(float(np.median(first_token_s)), 2),
-           "config": {"workload": "BASELINE configs[3]", "kv": "bf16 paged, 16-token pages", "sequences": n_seq, "prompt": "U[256,2048]",
+           "config": {"workload": "BASELINE configs[3]", "kv": "bf16 paged, 16-token pages", "gemm": args.gemm, "sequences": n_seq, "prompt": "U[256,2048]",
                       "chunk": chunk, "batch_token_budget": budget, "decode_tokens": n_out},
            "note": "a batch's decode rows run as one batched step through the MFMA GEMMs (per-row split-K "
                    "attention over each sequence's pages); prefill rows run chunked MFMA prefill"}
@@ -267,7 +267,7 @@ def run_config4(args):
     prompt = np.random.default_rng(0).integers(0, cfg["vocab"], args.c4_prompt).tolist()
     try:
         with ribn_amd.QwenRocm(path, context_tokens=args.c4_prompt + 256 + 16, max_sequences=1,
-                               max_batch_tokens=2048, kv="bf16") as m:
+                               max_batch_tokens=2048, kv="bf16", gemm=args.gemm) as m:
             info = m.info
             toks, tm = m.generate(prompt, 257)
     finally:
@@ -280,7 +280,7 @@ def run_config4(args):
            "ms_per_step": round(tm.decode_ms / 256, 3),
            "step_hbm": {"bytes_per_token": int(step_bytes),
                         "achieved_gbs": round(step_bytes / (tm.decode_ms / 256 / 1e3) / 1e9, 1)},
-           "config": {"workload": "BASELINE configs[4]", "kv": "bf16 paged, 16-token pages", "prompt": args.c4_prompt, "prefill_chunk": 2048,
+           "config": {"workload": "BASELINE configs[4]", "kv": "bf16 paged, 16-token pages", "gemm": args.gemm, "prompt": args.c4_prompt, "prefill_chunk": 2048,
                       "decode_tokens": 256, "layers": cfg["layers"]},
            "setup_s": {"synth": round(t_synth, 1)}}
     print(json.dumps(out))
@@ -333,6 +333,8 @@ def main():
                     help="2: the headline line (default); 1, 3 or 4: the configs[1] / [3] / [4] runs as their own line")
     ap.add_argument("--c3-tokens", type=int, default=256)
     ap.add_argument("--c4-prompt", type=int, default=32768)
+    ap.add_argument("--gemm", default="dequant", choices=["dequant", "resident"],
+                    help="configs[3]/[4]: prefill / batched-decode GEMM path (resident = binary16 weight copies)")
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: replays the gate/up, down and head "
@@ -391,6 +393,11 @@ def main():
         step_bytes, wbytes = algorithmic_bytes_per_token(info, args.prompt + args.steps / 2)
         step_gbs = step_bytes / (ms_per_step / 1e3) / 1e9
         m.close()
+        # the opt-in resident-weight GEMM path (binary16 weight copies, hipBLASLt) on the same prompt
+        with ribn_amd.QwenRocm(path, context_tokens=ctx, max_sequences=1, gemm="resident") as mr:
+            mr.generate(prompt, 2)
+            toks_r, tmr = mr.generate(prompt, 2)
+        prefill_res_tps = args.prompt / (tmr.prefill_ms / 1000.0)
         cpu = None if args.no_cpu else cpu_baseline(path, info)
         cpu_gemma = None if args.no_cpu else gemma_cpu_baseline()
         gemma_gpu = gemma_rocm_line()
@@ -418,6 +425,12 @@ def main():
         "prefill_mfma": {"achieved_tflops": round(2 * PARAMS_8B * prefill_tps / 1e12, 2), "peak_tflops": 2500.0,
                          "frac": round(2 * PARAMS_8B * prefill_tps / 1e12 / 2500.0, 4),
                          "note": "algorithmic matmul FLOPs (2 x matrix parameters per row) / prefill wall time"},
+        "prefill_resident_f16": {
+            "prefill_tok_s": round(prefill_res_tps, 2),
+            "mfma_frac": round(2 * PARAMS_8B * prefill_res_tps / 1e12 / 2500.0, 4),
+            "same_first_token": bool(toks_r[0] == toks[0]),
+            "note": "opt-in RIBN_LOAD_RESIDENT_F16: binary16 copies of the layer matrices and head made at load "
+                    "(+16.4 GB HBM), chunked prefill as hipBLASLt GEMMs; batch-1 decode unchanged"},
         "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
