@@ -607,6 +607,7 @@ hipError_t run_gemm(ribn_rocm_model* M, const PrefillGemm& g, const uint16_t* w1
                     hipStream_t st) {
     if (!M->blas || !w16) return launch_prefill_gemm(g, st);
     hipError_t e = blas_gemm(M->blas, g.x, g.m, g.k, w16, n, g.y, g.ldy, g.mode == MV_ADD, bias, st);
+    if (e == hipErrorNotSupported) return launch_prefill_gemm(g, st);   // no library kernel for this shape
     if (e != hipSuccess) return e;
     if (g.post == GEMM_POST_RMS_F16)
         return launch_rows_rms_f16(g.y, g.m, g.ldy, g.post_w, g.post_eps, true, g.post_out, g.ldy, st);
