@@ -26,10 +26,7 @@ typedef unsigned u4v_t __attribute__((ext_vector_type(4)));
 constexpr int kGemmThreads = 256;
 constexpr int kTileM = 128;   // chunk rows per workgroup
 constexpr int kTileK = 128;   // half a Q4_K / Q6_K super-block, four Q8_0 blocks
-#ifndef RIBN_PG_PAD
-#define RIBN_PG_PAD 8
-#endif
-constexpr int kLdsRow = kTileK + RIBN_PG_PAD;   // halves per LDS row (padded against bank conflicts)
+constexpr int kLdsRow = kTileK + 8;   // halves per LDS row (padded against bank conflicts)
 
 __device__ __forceinline__ float h2f_bits(uint32_t b) { return __half2float(__ushort_as_half((unsigned short)(b & 0xffffu))); }
 __device__ __forceinline__ float canon(uint32_t b) {
