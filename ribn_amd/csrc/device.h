@@ -16,6 +16,9 @@ typedef unsigned u4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+// matvec launches run 4 or 8 waves per workgroup (MvArgs::waves)
+constexpr int kMaxMvWaves = 8;
+constexpr int kMaxMvThreads = kMaxMvWaves * 64;
 
 __device__ __forceinline__ u4_t ld_nt16(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
@@ -179,7 +182,7 @@ template <int NP>
 __device__ __forceinline__ void stage_pre(const float* x, const float* norm_w, int k, XPre<NP>& p) {
 #pragma unroll
     for (int q = 0; q < NP; q++) {
-        const int g = q * kThreads + threadIdx.x;
+        const int g = q * (int)blockDim.x + threadIdx.x;
         const bool valid = g < k / 16;
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -262,6 +265,7 @@ template <int T, int NP = 0>
 __device__ __forceinline__ float stage_x(const float* x, const float* norm_w, float eps, int k, int8_t* xs, float* gs, float* red,
                          const XPre<NP == 0 ? 1 : NP>* pre = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = (int)blockDim.x;   // 256 or 512 threads (matvec launches choose)
     const float4* x4 = reinterpret_cast<const float4*>(x);
     const float4* w4 = reinterpret_cast<const float4*>(norm_w);
     const bool norm = norm_w != nullptr;
@@ -271,8 +275,8 @@ __device__ __forceinline__ float stage_x(const float* x, const float* norm_w, fl
     // four consecutive lanes, which share the block's scale
 #pragma unroll
     for (int q = 0; q < NP; q++) {
-        const int g = q * kThreads + tid;
-        if (q * kThreads < n16) {   // uniform
+        const int g = q * nt + tid;
+        if (q * nt < n16) {   // uniform
             float4 wl[4];
 #pragma unroll
             for (int j = 0; j < 4; j++)
@@ -280,7 +284,7 @@ __device__ __forceinline__ float stage_x(const float* x, const float* norm_w, fl
             stage_group<T>(g, k, pre->x[q], wl, norm, xs, gs, ss);
         }
     }
-    for (int base = NP * kThreads; base < n16; base += kThreads) {
+    for (int base = NP * nt; base < n16; base += nt) {
         const int g = base + tid;
         float4 xl[4], wl[4];
 #pragma unroll
@@ -297,7 +301,7 @@ __device__ __forceinline__ float stage_x(const float* x, const float* norm_w, fl
         __syncthreads();
         ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < kWaves; i++) ss += red[i];
+        for (int i = 0; i < (nt >> 6); i++) ss += red[i];
         inv = 1.0f / sqrtf(ss / (float)k + eps);
     }
     __syncthreads();
@@ -445,6 +449,7 @@ struct WaveWork {
     QMat wa;
     QMat wb;               // second row's matrix (the up matrix for gate/up pairs)
     int first_item, n_items, n_rows, ngr, n_units;
+    int stride;            // waves per workgroup: a wave's items are strided by it
     bool pair;
 };
 
@@ -455,7 +460,7 @@ struct WaveWork {
 template <int T>
 __device__ __forceinline__ void load_group(Group<T>& g, const WaveWork& w, int it, int gi) {
     using U = Unit<T>;
-    const int item = w.first_item + it * kWaves;
+    const int item = w.first_item + it * w.stride;
     const int ra = w.pair ? item : 2 * item;
     const int rb = w.pair ? item : min(ra + 1, w.n_rows - 1);
     const int lane = threadIdx.x & 63;
@@ -491,7 +496,7 @@ __device__ __forceinline__ float mv_addend(const MvSeg& sg, const WaveWork& w, i
     const int lane = threadIdx.x & 63;
     float v = 0.f;
     if (lane < 2 * w.n_items) {
-        const int item = w.first_item + (lane >> 1) * kWaves;
+        const int item = w.first_item + (lane >> 1) * w.stride;
         const int row = w.pair ? item : 2 * item + (lane & 1);
         if (row < w.n_rows && !(w.pair && (lane & 1))) {
             if (mode == MV_ADD) v = sg.res[row];
@@ -515,7 +520,7 @@ __device__ __forceinline__ void mv_finish(const MvSeg& sg, const WaveWork& w, co
     const float ya = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) * oscale;
     const float yb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) * oscale;
     a0 = b0 = 0.f;
-    const int item = w.first_item + c.it * kWaves;
+    const int item = w.first_item + c.it * w.stride;
     const int ra = w.pair ? item : 2 * item;
     const int rb = w.pair ? item : ra + 1;
     // (the host keeps a launch with addends at <= 32 items per wave)
@@ -669,9 +674,11 @@ __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uin
     w.wb = pair ? sg.w2 : sg.w;
     w.pair = pair;
     w.n_rows = (int)sg.w.rows;
-    w.first_item = lwg * sg.ipw * kWaves + wave;
+    const int nw = (int)blockDim.x >> 6;
+    w.stride = nw;
+    w.first_item = lwg * sg.ipw * nw + wave;
     const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
-    w.n_items = max(0, min(sg.ipw, (n_item_total - w.first_item + kWaves - 1) / kWaves));
+    w.n_items = max(0, min(sg.ipw, (n_item_total - w.first_item + nw - 1) / nw));
     if (si == 2 && TB != TA) return mv_run<TB, MODE, PB>(a, sg, w, xs, gs, red, best, sync);
     return mv_run<TA, MODE, PA>(a, sg, w, xs, gs, red, best, sync);
 }
@@ -681,7 +688,8 @@ __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uin
 // best key; the last to arrive reduces them and writes the token into the
 // active sequence (tokens[pos + 1], position advanced).
 __device__ __forceinline__ void head_finish(const MvArgs& a, uint64_t best, int wg, int n_wg) {
-    __shared__ uint64_t wbest[kWaves];
+    __shared__ uint64_t wbest[kMaxMvWaves];
+    const int nw = (int)blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) best = max(best, (uint64_t)__shfl_xor(best, o));
@@ -689,12 +697,12 @@ __device__ __forceinline__ void head_finish(const MvArgs& a, uint64_t best, int 
     __syncthreads();
     if (threadIdx.x == 0) {
         uint64_t b = wbest[0];
-        for (int i = 1; i < kWaves; i++) b = max(b, wbest[i]);
+        for (int i = 1; i < nw; i++) b = max(b, wbest[i]);
         st_agent(a.head.partial + wg, b);
     }
     if (arrive_last(a.head.counter, n_wg)) {
         uint64_t b = 0ull;
-        for (int i = threadIdx.x; i < n_wg; i += kThreads) b = max(b, ld_agent(a.head.partial + i));
+        for (int i = threadIdx.x; i < n_wg; i += (int)blockDim.x) b = max(b, ld_agent(a.head.partial + i));
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
         __syncthreads();
@@ -702,7 +710,7 @@ __device__ __forceinline__ void head_finish(const MvArgs& a, uint64_t best, int 
         __syncthreads();
         if (threadIdx.x == 0) {
             b = wbest[0];
-            for (int i = 1; i < kWaves; i++) b = max(b, wbest[i]);
+            for (int i = 1; i < nw; i++) b = max(b, wbest[i]);
             const uint32_t tok = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
             SeqState* s = a.ctl->seq;
             const int pos = s->pos;

@@ -105,6 +105,7 @@ struct MvArgs {
     int32_t mode;
     int32_t nseg;
     int32_t items_per_wave;  // default items per wave (item = 2 weight rows, or one gate/up pair)
+    int32_t waves;           // waves per workgroup of a standalone launch: 4 (0 means 4) or 8
     uint32_t type_a, type_b;
     MvSeg seg[3];
     HeadEpi head;

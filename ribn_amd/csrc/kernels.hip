@@ -85,7 +85,7 @@ constexpr int ring_standalone() {
 // two rows per item (or a gate/up pair); the first weight loads are issued
 // before the input is staged, so HBM streaming overlaps the prologue.
 template <int TA, int TB, int MODE>
-__global__ __launch_bounds__(kThreads) void matvec_kernel(MvArgs a) {
+__global__ __launch_bounds__(kMaxMvThreads) void matvec_kernel(MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     uint64_t best = 0ull;
     mv_wg<TA, TB, MODE, ring_standalone<TA>(), ring_standalone<TB>()>(a, blockIdx.x, lds, best, NoSync{});
@@ -235,6 +235,8 @@ hipError_t attention_dispatch(const AttnArgs& a, hipStream_t st) {
     }
 }
 
+int mv_waves(const MvArgs& a) { return a.waves ? a.waves : kWaves; }
+
 template <int MODE>
 hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
     const size_t lds = matvec_lds_bytes(a.k);
@@ -246,7 +248,7 @@ hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
             if (e != hipSuccess) return e;                                                         \
         }                                                                                          \
-        matvec_kernel<A, B, MODE><<<n_wg, kThreads, lds, st>>>(a);                                 \
+        matvec_kernel<A, B, MODE><<<n_wg, mv_waves(a) * 64, lds, st>>>(a);                                 \
         return hipGetLastError();                                                                  \
     }
     if constexpr (MODE == MV_STORE) {
@@ -261,10 +263,11 @@ hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
 
 size_t matvec_lds_bytes(int k) { return mv_red_offset(k) + 64 * 4; }
 
-int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * kWaves * (a.mode == MV_SILU ? 1 : 2); }
+int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * mv_waves(a) * (a.mode == MV_SILU ? 1 : 2); }
 
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
     if (n_wg <= 0 || a.k <= 0 || a.k % 16) return hipErrorInvalidValue;
+    if (a.waves != 0 && a.waves != 4 && a.waves != 8) return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; i++)   // per-row addends are held one per lane (mv_addend)
         if ((a.mode == MV_ADD || a.seg[i].bias) && a.seg[i].ipw > 32) return hipErrorInvalidValue;
     switch (a.mode) {

@@ -363,17 +363,37 @@ int ipw_env(const char* kind, int dflt) {
     const std::string key = std::string("RIBN_IPW_") + kind;
     const char* v = std::getenv(key.c_str());
     const int x = v ? std::atoi(v) : 0;
-    return x >= 1 && x <= 16 ? x : dflt;
+    return x >= 1 && x <= 64 ? x : dflt;
+}
+
+// Development knob: RIBN_WAVES_<KIND> sets the waves per workgroup (4 or 8) of one launch kind.
+int waves_env(const char* kind, int dflt) {
+    const std::string key = std::string("RIBN_WAVES_") + kind;
+    const char* v = std::getenv(key.c_str());
+    const int x = v ? std::atoi(v) : 0;
+    return x == 4 || x == 8 ? x : dflt;
+}
+
+// Items per wave that lay a launch of `items` out as at most one workgroup per
+// compute unit: measured on the 8B shape (gate/up, down, o, q|k|v), a launch whose
+// workgroups all start at once beats both smaller workgroups and a second round
+// (gate/up at 8 waves: 256 workgroups 13.4 us, 308 workgroups 18.6 us).
+int one_pass_ipw(int items, int waves, int n_cu) {
+    const int per = waves * std::max(n_cu, 1);
+    return std::min(16, std::max(1, (items + per - 1) / per));
 }
 
 void build_launches(ribn_rocm_model* M) {
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    int n_cu = 256;
+    hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, M->device);
     M->mv_qkv.clear(); M->mv_o.clear(); M->mv_gu.clear(); M->mv_down.clear();
     M->wg_qkv.clear(); M->wg_o.clear(); M->wg_gu.clear(); M->wg_down.clear();
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
-        q.items_per_wave = ipw_env("QKV", 2);
+        q.waves = waves_env("QKV", 8);
+        q.items_per_wave = ipw_env("QKV", one_pass_ipw((qd + 2 * kd) / 2, q.waves, n_cu));
         q.nseg = 3;
         q.type_a = y.q.type;
         q.type_b = y.v.type;
@@ -387,7 +407,8 @@ void build_launches(ribn_rocm_model* M) {
         o.nseg = 1;
         o.seg[0].w = y.o; o.seg[0].out = M->h;
         o.type_a = o.type_b = y.o.type;
-        o.items_per_wave = ipw_env("O", 1);
+        o.waves = waves_env("O", 8);
+        o.items_per_wave = ipw_env("O", one_pass_ipw(M->H / 2, o.waves, n_cu));
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
 
@@ -395,7 +416,8 @@ void build_launches(ribn_rocm_model* M) {
         g.nseg = 1;
         g.seg[0].w = y.gate; g.seg[0].w2 = y.up; g.seg[0].out = M->act;
         g.type_a = g.type_b = y.gate.type;
-        g.items_per_wave = ipw_env("GU", 4);
+        g.waves = waves_env("GU", 8);
+        g.items_per_wave = ipw_env("GU", one_pass_ipw(M->F, g.waves, n_cu));
         M->wg_gu.push_back(layout_segments(g));
         M->mv_gu.push_back(g);
 
@@ -403,7 +425,8 @@ void build_launches(ribn_rocm_model* M) {
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
         d.type_a = d.type_b = y.down.type;
-        d.items_per_wave = ipw_env("DOWN", 2);
+        d.waves = waves_env("DOWN", 8);
+        d.items_per_wave = ipw_env("DOWN", one_pass_ipw(M->H / 2, d.waves, n_cu));
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
@@ -412,6 +435,7 @@ void build_launches(ribn_rocm_model* M) {
     hdv.seg[0].w = M->out; hdv.seg[0].out = M->logits;
     hdv.type_a = hdv.type_b = M->out.type;
     hdv.items_per_wave = ipw_env("HEAD", choose_ipw(M->V / 2, 8));
+    hdv.waves = waves_env("HEAD", 4);
     hdv.head.partial = M->head_partial;
     hdv.head.counter = M->counters + M->hkv;
     M->head_wgs = layout_segments(hdv);
