@@ -378,9 +378,9 @@ int waves_env(const char* kind, int dflt) {
 // compute unit: measured on the 8B shape (gate/up, down, o, q|k|v), a launch whose
 // workgroups all start at once beats both smaller workgroups and a second round
 // (gate/up at 8 waves: 256 workgroups 13.4 us, 308 workgroups 18.6 us).
-int one_pass_ipw(int items, int waves, int n_cu) {
+int one_pass_ipw(int items, int waves, int n_cu, int cap = 16) {
     const int per = waves * std::max(n_cu, 1);
-    return std::min(16, std::max(1, (items + per - 1) / per));
+    return std::min(cap, std::max(1, (items + per - 1) / per));
 }
 
 void build_launches(ribn_rocm_model* M) {
@@ -434,8 +434,11 @@ void build_launches(ribn_rocm_model* M) {
     hdv.nseg = 1;
     hdv.seg[0].w = M->out; hdv.seg[0].out = M->logits;
     hdv.type_a = hdv.type_b = M->out.type;
-    hdv.items_per_wave = ipw_env("HEAD", choose_ipw(M->V / 2, 8));
-    hdv.waves = waves_env("HEAD", 4);
+    // the head also runs in a single pass of workgroups (8B, 151936 rows: 250
+    // workgroups of 8 waves x 38 items, 93.4 us against 99.0 us for 2374
+    // workgroups of 4 waves x 8 items); it has no addends, so no 32-item limit
+    hdv.waves = waves_env("HEAD", 8);
+    hdv.items_per_wave = ipw_env("HEAD", one_pass_ipw((M->V + 1) / 2, hdv.waves, n_cu, 64));
     hdv.head.partial = M->head_partial;
     hdv.head.counter = M->counters + M->hkv;
     M->head_wgs = layout_segments(hdv);
