@@ -27,7 +27,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel (layer gate/up matvec), from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # passes over `bench.py --probe-traffic`, FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a
 # 1 GiB device copy reads on the same counters). Summary and commands: profiles/hbm_traffic_matvec_qwen3_8b_q4km.md
-GATE_UP_TRAFFIC_BYTES = 58_700_000
+GATE_UP_TRAFFIC_BYTES = 59_180_000
 # parameters of every matrix a prompt row passes through (36 layers of q, k, v, o, gate, up, down; the head
 # runs for the final row only and is left out)
 PARAMS_8B = 36 * (4096 * (4096 + 1024 + 1024) + 4096 * 4096 + 3 * 4096 * 12288)
