@@ -300,10 +300,12 @@ MvArgs mv_base(const float* x, const float* norm_w, float eps, int k, int mode, 
 
 // Assign workgroups to segments; returns the grid size.
 int layout_segments(MvArgs& a) {
-    const int rpw = matvec_rows_per_wg(a);
+    const int rpi = matvec_rows_per_wg(a) / std::max(a.items_per_wave, 1);   // rows per item across the waves
     int wg = 0;
     for (int i = 0; i < a.nseg; i++) {
-        a.seg[i].ipw = a.items_per_wave;
+        // a segment keeps an items-per-wave count set beforehand (q|k|v balance)
+        if (a.seg[i].ipw <= 0) a.seg[i].ipw = a.items_per_wave;
+        const int rpw = rpi * a.seg[i].ipw;
         if (!a.seg[i].res) a.seg[i].res = a.seg[i].out;   // standalone launches add in place
         a.seg[i].wg_begin = wg;
         wg += ((int)a.seg[i].w.rows + rpw - 1) / rpw;
@@ -383,6 +385,13 @@ int one_pass_ipw(int items, int waves, int n_cu, int cap = 16) {
     return std::min(cap, std::max(1, (items + per - 1) / per));
 }
 
+// Encoded bytes of one row of a quantized matrix.
+double qrow_bytes(const QMat& w) {
+    uint64_t be = 1, bb = 0;
+    type_layout(w.type, &be, &bb);
+    return (double)w.k / (double)be * (double)bb;
+}
+
 void build_launches(ribn_rocm_model* M) {
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
     int n_cu = 256;
@@ -400,6 +409,15 @@ void build_launches(ribn_rocm_model* M) {
         q.seg[0].w = y.q; q.seg[0].out = M->raw; q.seg[0].bias = y.q_bias;
         q.seg[1].w = y.k; q.seg[1].out = M->raw + qd; q.seg[1].bias = y.k_bias;
         q.seg[2].w = y.v; q.seg[2].out = M->raw + qd + kd; q.seg[2].bias = y.v_bias;
+        {   // k and v: as many items per wave as keep a wave's bytes at most q's, so
+            // the smaller segments fill the CUs q leaves free without becoming the slowest
+            const char* b = std::getenv("RIBN_QKV_BALANCE");
+            if (!(b && b[0] == '0')) {
+                const double bq = qrow_bytes(y.q);
+                q.seg[1].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.k)));
+                q.seg[2].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.v)));
+            }
+        }
         M->wg_qkv.push_back(layout_segments(q));
         M->mv_qkv.push_back(q);
 
