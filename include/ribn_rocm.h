@@ -181,6 +181,16 @@ int ribn_rocm_trace(ribn_rocm_model *model, const uint32_t *tokens, uint32_t n, 
 int ribn_rocm_prefill_trace(ribn_rocm_model *model, const uint32_t *tokens, uint32_t n, uint32_t chunk,
                             float *logits_out, float *hidden_out, char *err, size_t err_len);
 
+/* Parity aid for batched decode (no reference counterpart; the reference's
+ * dispatcher returns only the sampled token per row, adapter.rs:90-125): after
+ * the last submission has been polled complete, copies the logits of the
+ * decode rows that submission ran as one batched step, in batch order, into
+ * out [n][vocab] and their sequence ids into sequences. *n_rows = 0 when the
+ * last submission ran no batched step. RIBN_ERR_INVALID if cap_rows is too
+ * small, RIBN_ERR_BUSY while a submission is pending. */
+int ribn_rocm_batch_logits(ribn_rocm_model *model, uint64_t *sequences, float *out, size_t cap_rows,
+                           size_t *n_rows, char *err, size_t err_len);
+
 /* ------------------------------------------------------------------------ */
 /* Kernel-level entry points (tests and bench). Host buffers in and out; the
  * weights go through the same load-time re-tiling as model tensors. */

@@ -660,7 +660,8 @@ static void gemv(uint32_t t, const uint8_t *w, int rows, int k, const float *x, 
     orc_gemv_q(t, w, (uint64_t)rows, (uint64_t)k, x, y, 1);
 }
 
-int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *trace, float *fnorm) {
+static int qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *trace, float *fnorm,
+                     int kv_only) {
     if (pos != m->pos_next || pos >= m->max_ctx || (int)token >= m->vocab) return ORC_ERR_CONFIG;
     int H = m->hidden, hd = m->hd, qd = m->hq * hd, kd = m->hkv * hd, F = m->ffn;
     float *h = (float *)malloc(sizeof(float) * H), *xn = (float *)malloc(sizeof(float) * H);
@@ -679,13 +680,14 @@ int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *tr
     for (int l = 0; l < m->layers; l++) {
         orc_layer *y = &m->L[l];
         orc_rms_norm(h, y->attn_norm, xn, H, m->eps);
-        gemv(y->tq, y->wq, qd, H, xn, q);
+        const int last_kv = kv_only && l == m->layers - 1;   /* q is not needed */
+        if (!last_kv) gemv(y->tq, y->wq, qd, H, xn, q);
         gemv(y->tk, y->wk, kd, H, xn, k);
         gemv(y->tv, y->wv, kd, H, xn, v);
-        if (y->q_bias) for (int i = 0; i < qd; i++) q[i] = q[i] + y->q_bias[i];
+        if (y->q_bias && !last_kv) for (int i = 0; i < qd; i++) q[i] = q[i] + y->q_bias[i];
         if (y->k_bias) for (int i = 0; i < kd; i++) k[i] = k[i] + y->k_bias[i];
         if (y->v_bias) for (int i = 0; i < kd; i++) v[i] = v[i] + y->v_bias[i];
-        if (y->q_norm)
+        if (y->q_norm && !last_kv)
             for (int hh = 0; hh < m->hq; hh++) {
                 orc_rms_norm(q + hh * hd, y->q_norm, tmp, hd, m->eps);
                 memcpy(q + hh * hd, tmp, sizeof(float) * hd);
@@ -695,12 +697,13 @@ int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *tr
                 orc_rms_norm(k + hh * hd, y->k_norm, tmp, hd, m->eps);
                 memcpy(k + hh * hd, tmp, sizeof(float) * hd);
             }
-        orc_rope_neox(q, m->hq, hd, m->rot, pos, m->base);
+        if (!last_kv) orc_rope_neox(q, m->hq, hd, m->rot, pos, m->base);
         orc_rope_neox(k, m->hkv, hd, m->rot, pos, m->base);
         memcpy(y->kcache + (size_t)pos * kd, k, sizeof(float) * kd);
         memcpy(y->vcache + (size_t)pos * kd, v, sizeof(float) * kd);
         kv_round(y->kcache + (size_t)pos * kd, kd, m->kv_round);
         kv_round(y->vcache + (size_t)pos * kd, kd, m->kv_round);
+        if (kv_only && l == m->layers - 1) break;   /* nothing after the last cache append is needed */
         int tokens = pos + 1;
         for (int qh = 0; qh < m->hq; qh++) {
             int kh = qh / group;
@@ -733,11 +736,21 @@ int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *tr
         for (int i = 0; i < H; i++) h[i] = h[i] + o[i];
         if (trace) memcpy(trace + (size_t)(l + 1) * H, h, sizeof(float) * H);
     }
-    orc_rms_norm(h, m->out_norm, xn, H, m->eps);
-    if (fnorm) memcpy(fnorm, xn, sizeof(float) * H);
-    if (logits) gemv(m->t_out, m->out, m->vocab, H, xn, logits);
+    if (!kv_only) {
+        orc_rms_norm(h, m->out_norm, xn, H, m->eps);
+        if (fnorm) memcpy(fnorm, xn, sizeof(float) * H);
+        if (logits) gemv(m->t_out, m->out, m->vocab, H, xn, logits);
+    }
     m->pos_next = pos + 1;
     free(h); free(xn); free(q); free(k); free(v); free(att); free(o); free(gt); free(up);
     free(sc); free(tmp);
     return ORC_OK;
+}
+
+int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *trace, float *fnorm) {
+    return qwen_step(m, token, pos, logits, trace, fnorm, 0);
+}
+
+int orc_qwen_append_kv(orc_qwen *m, uint32_t token, int pos) {
+    return qwen_step(m, token, pos, NULL, NULL, NULL, 1);
 }

@@ -96,6 +96,12 @@ void orc_qwen_config(const orc_qwen *m, int32_t *cfg8, float *eps, float *rope_b
  * layer. final_norm (hidden floats) may be NULL. */
 int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *hidden_trace,
                   float *final_norm);
+/* Advance one position writing only what later positions read: every layer's
+ * K/V cache entry. Layers before the last still run in full (their outputs feed
+ * the next layer's K/V); the last layer stops after its cache append, and no
+ * readout is computed. Equal to orc_qwen_step for every later position's
+ * result, at a fraction of the cost on 1-layer models (long-context tests). */
+int orc_qwen_append_kv(orc_qwen *m, uint32_t token, int pos);
 void orc_qwen_reset(orc_qwen *m);
 /* Round K/V as they enter the cache: 0 = keep f32 (reference host equations),
  * 1 = binary16 RNE (the reference CUDA cache, model_ops.rs:1210-1276),

@@ -132,6 +132,8 @@ _sig("ribn_rocm_synchronize", _c.c_int, _c.c_void_p, _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_generate", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _c.c_uint32, _u32p, _c.POINTER(Timing),
      _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_trace", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _u32p, _f32p, _f32p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_batch_logits", _c.c_int, _c.c_void_p, _c.POINTER(_c.c_uint64), _f32p, _c.c_size_t,
+     _c.POINTER(_c.c_size_t), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_dequantize", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_gemv", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _f32p, _c.c_float, _f32p,
      _c.c_char_p, _c.c_size_t)
@@ -356,6 +358,17 @@ class QwenRocm:
             return None
         return [StepCompletion(out[i].sequence, out[i].prefix, (out[i].token,) if out[i].n_tokens else ())
                 for i in range(n.value)]
+
+    def batch_logits(self):
+        """Logits of the decode rows the last completed submission ran as one batched step:
+        (sequence ids, [rows][vocab]); empty when it ran none."""
+        cap = max(1, self.info.max_sequences)
+        seqs = np.zeros(cap, dtype=np.uint64)
+        out = np.zeros((cap, self.info.vocab), dtype=np.float32)
+        n = ctypes.c_size_t()
+        self._call(_lib.ribn_rocm_batch_logits, seqs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                   _ptr(out, _f32p), cap, ctypes.byref(n))
+        return seqs[: n.value].tolist(), out[: n.value].copy()
 
     def release(self, sequence: int) -> None:
         self._call(_lib.ribn_rocm_release, sequence)

@@ -118,6 +118,7 @@ struct ribn_rocm_model {
     std::vector<int32_t> h_brows;
     uint32_t* d_btokens = nullptr;
     float *b_att = nullptr, *b_rope = nullptr, *b_part = nullptr, *b_logits = nullptr;
+    std::vector<uint64_t> last_batch_seqs;   // sequences of the last submission's batched decode rows
     size_t b_part_stride = 0;
     uint32_t* b_counters = nullptr;
     size_t p_part_floats = 0;
@@ -360,22 +361,6 @@ int layout_grid(MvArgs& a, int n_wg) {
     return wg;
 }
 
-// Development knob: RIBN_IPW_<KIND> overrides the items per wave of one launch kind.
-int ipw_env(const char* kind, int dflt) {
-    const std::string key = std::string("RIBN_IPW_") + kind;
-    const char* v = std::getenv(key.c_str());
-    const int x = v ? std::atoi(v) : 0;
-    return x >= 1 && x <= 64 ? x : dflt;
-}
-
-// Development knob: RIBN_WAVES_<KIND> sets the waves per workgroup (4 or 8) of one launch kind.
-int waves_env(const char* kind, int dflt) {
-    const std::string key = std::string("RIBN_WAVES_") + kind;
-    const char* v = std::getenv(key.c_str());
-    const int x = v ? std::atoi(v) : 0;
-    return x == 4 || x == 8 ? x : dflt;
-}
-
 // Items per wave that lay a launch of `items` out as at most one workgroup per
 // compute unit: measured on the 8B shape (gate/up, down, o, q|k|v), a launch whose
 // workgroups all start at once beats both smaller workgroups and a second round
@@ -401,8 +386,8 @@ void build_launches(ribn_rocm_model* M) {
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
-        q.waves = waves_env("QKV", 8);
-        q.items_per_wave = ipw_env("QKV", one_pass_ipw((qd + 2 * kd) / 2, q.waves, n_cu));
+        q.waves = 8;
+        q.items_per_wave = one_pass_ipw((qd + 2 * kd) / 2, q.waves, n_cu);
         q.nseg = 3;
         q.type_a = y.q.type;
         q.type_b = y.v.type;
@@ -411,12 +396,9 @@ void build_launches(ribn_rocm_model* M) {
         q.seg[2].w = y.v; q.seg[2].out = M->raw + qd + kd; q.seg[2].bias = y.v_bias;
         {   // k and v: as many items per wave as keep a wave's bytes at most q's, so
             // the smaller segments fill the CUs q leaves free without becoming the slowest
-            const char* b = std::getenv("RIBN_QKV_BALANCE");
-            if (!(b && b[0] == '0')) {
-                const double bq = qrow_bytes(y.q);
-                q.seg[1].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.k)));
-                q.seg[2].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.v)));
-            }
+            const double bq = qrow_bytes(y.q);
+            q.seg[1].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.k)));
+            q.seg[2].ipw = std::max(1, (int)(q.items_per_wave * bq / qrow_bytes(y.v)));
         }
         M->wg_qkv.push_back(layout_segments(q));
         M->mv_qkv.push_back(q);
@@ -425,8 +407,8 @@ void build_launches(ribn_rocm_model* M) {
         o.nseg = 1;
         o.seg[0].w = y.o; o.seg[0].out = M->h;
         o.type_a = o.type_b = y.o.type;
-        o.waves = waves_env("O", 8);
-        o.items_per_wave = ipw_env("O", one_pass_ipw(M->H / 2, o.waves, n_cu));
+        o.waves = 8;
+        o.items_per_wave = one_pass_ipw(M->H / 2, o.waves, n_cu);
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
 
@@ -434,8 +416,8 @@ void build_launches(ribn_rocm_model* M) {
         g.nseg = 1;
         g.seg[0].w = y.gate; g.seg[0].w2 = y.up; g.seg[0].out = M->act;
         g.type_a = g.type_b = y.gate.type;
-        g.waves = waves_env("GU", 8);
-        g.items_per_wave = ipw_env("GU", one_pass_ipw(M->F, g.waves, n_cu));
+        g.waves = 8;
+        g.items_per_wave = one_pass_ipw(M->F, g.waves, n_cu);
         M->wg_gu.push_back(layout_segments(g));
         M->mv_gu.push_back(g);
 
@@ -443,8 +425,8 @@ void build_launches(ribn_rocm_model* M) {
         d.nseg = 1;
         d.seg[0].w = y.down; d.seg[0].out = M->h;
         d.type_a = d.type_b = y.down.type;
-        d.waves = waves_env("DOWN", 8);
-        d.items_per_wave = ipw_env("DOWN", one_pass_ipw(M->H / 2, d.waves, n_cu));
+        d.waves = 8;
+        d.items_per_wave = one_pass_ipw(M->H / 2, d.waves, n_cu);
         M->wg_down.push_back(layout_segments(d));
         M->mv_down.push_back(d);
     }
@@ -455,8 +437,8 @@ void build_launches(ribn_rocm_model* M) {
     // the head also runs in a single pass of workgroups (8B, 151936 rows: 250
     // workgroups of 8 waves x 38 items, 93.4 us against 99.0 us for 2374
     // workgroups of 4 waves x 8 items); it has no addends, so no 32-item limit
-    hdv.waves = waves_env("HEAD", 8);
-    hdv.items_per_wave = ipw_env("HEAD", one_pass_ipw((M->V + 1) / 2, hdv.waves, n_cu, 64));
+    hdv.waves = 8;
+    hdv.items_per_wave = one_pass_ipw((M->V + 1) / 2, hdv.waves, n_cu, 64);
     hdv.head.partial = M->head_partial;
     hdv.head.counter = M->counters + M->hkv;
     M->head_wgs = layout_segments(hdv);
@@ -1466,6 +1448,7 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
     if (!M->pending.done) e = hipEventCreateWithFlags(&M->pending.done, hipEventDisableTiming);
     // decode rows (one token, sampled) of two or more sequences run as one batched step
     std::vector<char> batched(n, 0);
+    M->last_batch_seqs.clear();
     if (M->b_rows >= 2 && M->step_wg == 0) {
         std::vector<int> bslots, bpos;
         std::vector<size_t> brow;
@@ -1482,6 +1465,8 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
                 batched[brow[i]] = 1;
                 M->seqs[items[brow[i]].sequence].in_flight = true;
             }
+            M->last_batch_seqs.clear();
+            for (size_t i = 0; i < brow.size(); i++) M->last_batch_seqs.push_back(items[brow[i]].sequence);
             e = decode_rows(M, bslots, bpos);
             for (size_t i = 0; e == hipSuccess && i < brow.size(); i++)
                 e = hipMemcpyAsync(&M->h_out[brow[i]], &M->d_slots[bslots[i]].last_token, 4, hipMemcpyDeviceToHost,
@@ -1513,6 +1498,21 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
     M->has_pending = true;
     if (e != hipSuccess) return fail(M, err, err_len, hip_msg("submit", e));
     *submission = M->pending.id;
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_batch_logits(ribn_rocm_model* M, uint64_t* sequences, float* out, size_t cap_rows,
+                                      size_t* n_rows, char* err, size_t err_len) {
+    if (!M || !n_rows) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    const size_t n = M->last_batch_seqs.size();
+    *n_rows = n;
+    if (n == 0) return RIBN_OK;
+    if (cap_rows < n || !out || !sequences) return fail(nullptr, err, err_len, "output too small", RIBN_ERR_INVALID);
+    for (size_t i = 0; i < n; i++) sequences[i] = M->last_batch_seqs[i];
+    hipError_t e = hipMemcpyAsync(out, M->b_logits, sizeof(float) * n * M->V, hipMemcpyDeviceToHost, M->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(M->stream);
+    if (e != hipSuccess) return fail(M, err, err_len, hip_msg("batch_logits", e));
     return RIBN_OK;
 }
 

@@ -46,6 +46,7 @@ def lib():
         _lib.orc_qwen_close.argtypes = [c.c_void_p]
         _lib.orc_qwen_config.argtypes = [c.c_void_p, c.c_void_p, c.POINTER(c.c_float), c.POINTER(c.c_float)]
         _lib.orc_qwen_step.argtypes = [c.c_void_p, c.c_uint32, c.c_int, c.c_void_p, c.c_void_p, c.c_void_p]
+        _lib.orc_qwen_append_kv.argtypes = [c.c_void_p, c.c_uint32, c.c_int]
         _lib.orc_qwen_reset.argtypes = [c.c_void_p]
         _lib.orc_qwen_set_kv_round.argtypes = [c.c_void_p, c.c_int]
         _lib.orc_round_f16.restype = c.c_float
@@ -175,6 +176,11 @@ class QwenOracle:
         assert rc == 0, rc
         self.pos += 1
         return logits, hid
+
+    def append_kv(self, token):
+        """Advance one position, writing the K/V cache entries only (no readout)."""
+        assert lib().orc_qwen_append_kv(self.h, int(token), self.pos) == 0
+        self.pos += 1
 
     def reset(self):
         lib().orc_qwen_reset(self.h)

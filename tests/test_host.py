@@ -165,3 +165,27 @@ def test_oracle_forward_matches_fp64_brute_force(tmp_path, qwen3, wt):
     o.close()
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert rel < 1e-5, rel
+
+
+@pytest.mark.parametrize("layers", [1, 2])
+def test_oracle_append_kv_equals_full_steps(tmp_path, layers):
+    """orc_qwen_append_kv (K/V only, no readout) leaves the oracle in the state full steps do: the logits of
+    every later position are bit-identical, and so is the FP64 brute force's agreement."""
+    p = str(tmp_path / "kv.gguf")
+    ribn_amd.synth_qwen_gguf(p, qwen3=True, hidden=256, layers=layers, q_heads=8, kv_heads=1, head_dim=128,
+                             ffn=512, vocab=128, seed=13, norm_jitter=0.2, weight_std=0.05)
+    toks = [3, 77, 5, 120, 9, 64, 11, 100, 2]
+    for kv_round in (0, 2):
+        full = orc.QwenOracle(p, max_ctx=16, kv_round=kv_round)
+        part = orc.QwenOracle(p, max_ctx=16, kv_round=kv_round)
+        ref = [full.step(t)[0] for t in toks]
+        for t in toks[:6]:
+            part.append_kv(t)
+        got = [part.step(t)[0] for t in toks[6:]]
+        full.close()
+        part.close()
+        for a, b in zip(got, ref[6:]):
+            assert np.array_equal(a, b)
+    cfg, W = _load_fp64(p)
+    fp64 = _fp64_forward(cfg, W, toks)
+    assert np.linalg.norm(np.stack(got) - fp64[6:]) / np.linalg.norm(fp64[6:]) < 5e-3   # kv_round 2: bf16 cache
