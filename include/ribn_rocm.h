@@ -216,6 +216,20 @@ int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t *blocks, uint64_t rows, 
 /* Greedy argmax (model_ops.rs:203-260): first maximum, NaN skipped. */
 int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, size_t err_len);
 
+/* Allocation-free greedy argmax. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same kernel and result
+ * as ribn_rocm_argmax, but d_logits (n floats) and d_out (one uint32) are device
+ * pointers on the current device, and the work is enqueued on `stream` (a
+ * hipStream_t; NULL = the default stream) without synchronizing. It calls no
+ * allocator: the cross-workgroup partials and arrival counter live in a fixed
+ * 8.4 KB device array per GPU, held until the process ends. Calls that overlap
+ * on one GPU share that array and race; serialize them (one stream, or events).
+ * n above RIBN_ARGMAX_NOALLOC_MAX returns RIBN_ERR_INVALID. */
+#define RIBN_ARGMAX_NOALLOC_MAX 0x7fffffffull
+int ribn_rocm_argmax_noalloc(const float *d_logits, uint64_t n, uint32_t *d_out, void *stream, char *err,
+                             size_t err_len);
+
 /* Model-resident timing of one launch of the decode chain, replayed `iters`
  * times on the model's stream: which = 0 fused gate/up (SwiGLU) of layer 0,
  * 1 ffn_down, 2 output head, 3 and 4 fused QKV, 5 attn_output, 6 decode attention of layer 0 (pass the context
