@@ -63,13 +63,19 @@ typedef struct {
 #define RIBN_LOAD_KV_BF16 1u
 /* Run each token step as one persistent kernel launch (grid barriers between the
  * stages) when one is compiled for the model's configuration, instead of the
- * default chain of per-stage launches replayed as HIP graphs. */
+ * default chain of per-stage launches replayed as HIP graphs. Measured slower
+ * than the default; kept as an opt-in. Every grid-barrier wait is bounded (2 s):
+ * a wait that runs out makes every kernel exit, the call returns RIBN_ERR_DEVICE
+ * and the handle is faulted (every later call returns RIBN_ERR_FAULTED), as a
+ * device error faults QwenExecution (qwen/src/execution.rs:305-316). The caller
+ * frees the handle and loads the model again. */
 #define RIBN_LOAD_PERSISTENT_STEP 2u
 /* Keep a binary16 copy of every layer matrix and of the output head, dequantized
  * once at load (exactly, then rounded to binary16), and run chunked prefill and
  * batched decode as plain hipBLASLt GEMMs on it instead of the dequantizing MFMA
  * GEMM. Costs 2 bytes per weight of extra HBM (16.4 GB for an 8B model); the
- * batch-1 decode matvecs keep streaming the GGUF planes. */
+ * batch-1 decode matvecs keep streaming the GGUF planes. libhipblaslt.so is
+ * opened at load only when this flag is set (RIBN_ERR_DEVICE if it cannot be). */
 #define RIBN_LOAD_RESIDENT_F16 4u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,

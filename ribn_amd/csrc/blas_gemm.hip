@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <dlfcn.h>
+
 #include <map>
 #include <tuple>
 
@@ -34,46 +36,87 @@ struct BlasGemm {
 
 namespace {
 
+// hipBLASLt is opened on first use (dlopen), so the library does not depend on
+// it unless the resident-weight mode runs.
+struct LtApi {
+    decltype(&::hipblasLtCreate) Create = nullptr;
+    decltype(&::hipblasLtDestroy) Destroy = nullptr;
+    decltype(&::hipblasLtMatmul) Matmul = nullptr;
+    decltype(&::hipblasLtMatmulAlgoGetHeuristic) MatmulAlgoGetHeuristic = nullptr;
+    decltype(&::hipblasLtMatmulDescCreate) MatmulDescCreate = nullptr;
+    decltype(&::hipblasLtMatmulDescDestroy) MatmulDescDestroy = nullptr;
+    decltype(&::hipblasLtMatmulDescSetAttribute) MatmulDescSetAttribute = nullptr;
+    decltype(&::hipblasLtMatmulPreferenceCreate) MatmulPreferenceCreate = nullptr;
+    decltype(&::hipblasLtMatmulPreferenceDestroy) MatmulPreferenceDestroy = nullptr;
+    decltype(&::hipblasLtMatmulPreferenceSetAttribute) MatmulPreferenceSetAttribute = nullptr;
+    decltype(&::hipblasLtMatrixLayoutCreate) MatrixLayoutCreate = nullptr;
+    decltype(&::hipblasLtMatrixLayoutDestroy) MatrixLayoutDestroy = nullptr;
+};
+
+const LtApi* lt_api() {
+    static const LtApi* api = [] {
+        void* h = dlopen("libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
+        if (!h) h = dlopen("/opt/rocm/lib/libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
+        if (!h) return static_cast<const LtApi*>(nullptr);
+        static LtApi a;
+        bool ok = true;
+        ok = ok && (a.Create = reinterpret_cast<decltype(&::hipblasLtCreate)>(dlsym(h, "hipblasLtCreate")));
+        ok = ok && (a.Destroy = reinterpret_cast<decltype(&::hipblasLtDestroy)>(dlsym(h, "hipblasLtDestroy")));
+        ok = ok && (a.Matmul = reinterpret_cast<decltype(&::hipblasLtMatmul)>(dlsym(h, "hipblasLtMatmul")));
+        ok = ok && (a.MatmulAlgoGetHeuristic = reinterpret_cast<decltype(&::hipblasLtMatmulAlgoGetHeuristic)>(dlsym(h, "hipblasLtMatmulAlgoGetHeuristic")));
+        ok = ok && (a.MatmulDescCreate = reinterpret_cast<decltype(&::hipblasLtMatmulDescCreate)>(dlsym(h, "hipblasLtMatmulDescCreate")));
+        ok = ok && (a.MatmulDescDestroy = reinterpret_cast<decltype(&::hipblasLtMatmulDescDestroy)>(dlsym(h, "hipblasLtMatmulDescDestroy")));
+        ok = ok && (a.MatmulDescSetAttribute = reinterpret_cast<decltype(&::hipblasLtMatmulDescSetAttribute)>(dlsym(h, "hipblasLtMatmulDescSetAttribute")));
+        ok = ok && (a.MatmulPreferenceCreate = reinterpret_cast<decltype(&::hipblasLtMatmulPreferenceCreate)>(dlsym(h, "hipblasLtMatmulPreferenceCreate")));
+        ok = ok && (a.MatmulPreferenceDestroy = reinterpret_cast<decltype(&::hipblasLtMatmulPreferenceDestroy)>(dlsym(h, "hipblasLtMatmulPreferenceDestroy")));
+        ok = ok && (a.MatmulPreferenceSetAttribute = reinterpret_cast<decltype(&::hipblasLtMatmulPreferenceSetAttribute)>(dlsym(h, "hipblasLtMatmulPreferenceSetAttribute")));
+        ok = ok && (a.MatrixLayoutCreate = reinterpret_cast<decltype(&::hipblasLtMatrixLayoutCreate)>(dlsym(h, "hipblasLtMatrixLayoutCreate")));
+        ok = ok && (a.MatrixLayoutDestroy = reinterpret_cast<decltype(&::hipblasLtMatrixLayoutDestroy)>(dlsym(h, "hipblasLtMatrixLayoutDestroy")));
+        return ok ? static_cast<const LtApi*>(&a) : nullptr;
+    }();
+    return api;
+}
+
 constexpr size_t kWorkspaceBytes = 64ull << 20;
 
 hipError_t to_hip(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS ? hipSuccess : hipErrorUnknown; }
 
 void destroy_plan(BlasGemm::Plan& p) {
-    if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
-    if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
-    if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
-    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+    if (p.a) lt_api()->MatrixLayoutDestroy(p.a);
+    if (p.b) lt_api()->MatrixLayoutDestroy(p.b);
+    if (p.c) lt_api()->MatrixLayoutDestroy(p.c);
+    if (p.desc) lt_api()->MatmulDescDestroy(p.desc);
     p = BlasGemm::Plan{};
 }
 
 hipError_t make_plan(BlasGemm* g, int m, int n, int k, int ldy, bool add, bool bias, BlasGemm::Plan* out) {
     BlasGemm::Plan p;
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    hipblasStatus_t s = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    hipblasStatus_t s = lt_api()->MatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+        s = lt_api()->MatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+        s = lt_api()->MatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
     if (s == HIPBLAS_STATUS_SUCCESS && bias) {
         const hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
         const hipDataType bt = HIP_R_32F;
-        s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
+        s = lt_api()->MatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
         if (s == HIPBLAS_STATUS_SUCCESS)
-            s = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+            s = lt_api()->MatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
     }
-    if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, k, n, k);
-    if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, k, m, k);
-    if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatrixLayoutCreate(&p.c, HIP_R_32F, n, m, ldy);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = lt_api()->MatrixLayoutCreate(&p.a, HIP_R_16F, k, n, k);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = lt_api()->MatrixLayoutCreate(&p.b, HIP_R_16F, k, m, k);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = lt_api()->MatrixLayoutCreate(&p.c, HIP_R_32F, n, m, ldy);
     hipblasLtMatmulPreference_t pref = nullptr;
-    if (s == HIPBLAS_STATUS_SUCCESS) s = hipblasLtMatmulPreferenceCreate(&pref);
+    if (s == HIPBLAS_STATUS_SUCCESS) s = lt_api()->MatmulPreferenceCreate(&pref);
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &g->ws_bytes,
+        s = lt_api()->MatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &g->ws_bytes,
                                                   sizeof(g->ws_bytes));
     hipblasLtMatmulHeuristicResult_t res[1];
     int found = 0;
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, res, &found);
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        s = lt_api()->MatmulAlgoGetHeuristic(g->handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, res, &found);
+    if (pref) lt_api()->MatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS || found < 1) {
         destroy_plan(p);
         return hipErrorNotSupported;
@@ -88,8 +131,9 @@ hipError_t make_plan(BlasGemm* g, int m, int n, int k, int ldy, bool add, bool b
 
 hipError_t blas_create(BlasGemm** out, hipStream_t stream) {
     (void)stream;
+    if (!lt_api()) return hipErrorSharedObjectInitFailed;   // libhipblaslt.so not loadable
     BlasGemm* g = new BlasGemm();
-    hipError_t e = to_hip(hipblasLtCreate(&g->handle));
+    hipError_t e = to_hip(lt_api()->Create(&g->handle));
     if (e == hipSuccess) e = hipMalloc(&g->workspace, kWorkspaceBytes);
     if (e != hipSuccess) {
         blas_destroy(g);
@@ -104,7 +148,7 @@ void blas_destroy(BlasGemm* g) {
     if (!g) return;
     for (auto& kv : g->plans) destroy_plan(kv.second);
     if (g->workspace) (void)hipFree(g->workspace);
-    if (g->handle) hipblasLtDestroy(g->handle);
+    if (g->handle) lt_api()->Destroy(g->handle);
     delete g;
 }
 
@@ -122,11 +166,11 @@ hipError_t blas_gemm(BlasGemm* g, const uint16_t* x, int m, int k, const uint16_
     BlasGemm::Plan& p = it->second;
     if (bias) {
         const hipblasStatus_t s =
-            hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
+            lt_api()->MatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
         if (s != HIPBLAS_STATUS_SUCCESS) return hipErrorUnknown;
     }
     const float alpha = 1.0f, beta = add ? 1.0f : 0.0f;
-    return to_hip(hipblasLtMatmul(g->handle, p.desc, &alpha, w16, p.a, x, p.b, &beta, y, p.c, y, p.c, &p.algo,
+    return to_hip(lt_api()->Matmul(g->handle, p.desc, &alpha, w16, p.a, x, p.b, &beta, y, p.c, y, p.c, &p.algo,
                                   g->workspace, g->ws_bytes, stream));
 }
 

@@ -569,10 +569,14 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
                                         float* red, uint64_t& best, Sync&& sync) {
     const int total = w.n_items * w.ngr;
     constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX;
-    // the residual launches (O, down) take a long input without norm: three passes early
-    constexpr int NP = EARLY ? (MODE == MV_ADD ? 3 : 1) : 0;
+    // the residual launches (O, down) take a long input without norm: four passes
+    // early (k up to 32768 at 512 threads). Their norm weights are a compile-time
+    // null, so no staging pass holds a conditional load, whose wait would cover the
+    // weight loads in flight as well.
+    constexpr int NP = EARLY ? (MODE == MV_ADD ? 4 : 1) : 0;
+    const float* const norm_w = MODE == MV_ADD ? nullptr : a.norm_w;
     XPre<NP == 0 ? 1 : NP> pre;
-    if constexpr (NP > 0) stage_pre<NP>(a.x, a.norm_w, a.k, pre);
+    if constexpr (NP > 0) stage_pre<NP>(a.x, norm_w, a.k, pre);
     const float addend = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE) : 0.f;
     Group<T> ring[D];
     Cursor ld{0, 0};
@@ -584,7 +588,6 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     int ldq = D;   // index of the group `ld` points at
     if (!sync()) return false;
     const float* const x = a.x;
-    const float* const norm_w = a.norm_w;
     const float eps = a.eps;
     const int k = a.k;
     const float oscale = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);

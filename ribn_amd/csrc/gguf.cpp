@@ -123,6 +123,8 @@ std::string GgufFile::open(const std::string& path) {
         t.type = (uint32_t)r.uint(4);
         t.offset = r.uint(8);
         if (!r.err.empty()) break;
+        // a second tensor of one name would be unreachable by lookup: rejected
+        if (index_.count(t.name)) return "duplicate tensor name " + t.name;
         index_[t.name] = tensors_.size();
         tensors_.push_back(std::move(t));
     }
@@ -141,12 +143,15 @@ std::string GgufFile::open(const std::string& path) {
         if (t.offset > len_ - off) return "tensor " + t.name + " offset " + std::to_string(t.offset) + " is out of bounds";
         uint64_t be, bb;
         if (type_layout(t.type, &be, &bb) && !t.dims.empty()) {
+            // checked products, as TensorInfo::byte_len (crates/gguf/src/lib.rs:142-168):
+            // an element count or byte length that overflows u64 is an error
             uint64_t n = 1;
-            for (auto d : t.dims) n *= d;
+            for (auto d : t.dims)
+                if (__builtin_mul_overflow(n, d, &n)) return "tensor " + t.name + " element count overflows";
             if (t.dims[0] % be || n % be)
                 return "tensor " + t.name + " dimension " + std::to_string(t.dims[0]) + " is not a multiple of " +
                        std::to_string(be);
-            t.bytes = n / be * bb;
+            if (__builtin_mul_overflow(n / be, bb, &t.bytes)) return "tensor " + t.name + " byte length overflows";
             if (t.bytes > len_ - off - t.offset) return "tensor " + t.name + " extends past the end of the file";
         }
     }

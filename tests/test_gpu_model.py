@@ -75,7 +75,9 @@ def _oracle_trace(path, tokens, ctx, hidden=False, kv_round=0):
     return np.stack(ls), (np.stack(hs) if hidden else None)
 
 
-STEPS = ["persistent", "chain"]
+# the opt-in persistent step runs one parity test (test_persistent_step_trace); every other test runs the
+# default launch chain
+STEPS = ["chain"]
 # (model, kv) configurations without a compiled persistent step kernel: they run the launch chain
 NO_STEP_KERNEL = {("qwen3_g8_tied", "bf16")}
 
@@ -120,6 +122,14 @@ def test_trace_hidden_and_logits(model_paths, name, kv, step):
             margin = ref_l[p][o_pick] - ref_l[p][am[p]]
             assert margin <= 4 * err, f"pos {p}: argmax {am[p]} vs {o_pick}, margin {margin:.3e}"
         assert am[p] == orc.argmax(lg[p])   # the device argmax is the argmax of the device logits
+
+
+@pytest.mark.parametrize("kv", list(KV_MODES))
+@pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen2_q8_0_g7"])
+def test_persistent_step_trace(model_paths, name, kv):
+    """The opt-in persistent step (one launch per token, grid barriers between stages): per-layer hidden states,
+    logits and argmax against the oracle, as test_trace_hidden_and_logits does for the launch chain."""
+    test_trace_hidden_and_logits(model_paths, name, kv, "persistent")
 
 
 @pytest.mark.parametrize("gemm", ["dequant", "resident"])

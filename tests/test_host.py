@@ -189,3 +189,37 @@ def test_oracle_append_kv_equals_full_steps(tmp_path, layers):
     cfg, W = _load_fp64(p)
     fp64 = _fp64_forward(cfg, W, toks)
     assert np.linalg.norm(np.stack(got) - fp64[6:]) / np.linalg.norm(fp64[6:]) < 5e-3   # kv_round 2: bf16 cache
+
+
+def _gguf_bytes(tensors, arch="qwen3"):
+    """A minimal GGUF v3 stream: one metadata key and the given (name, dims, type, offset) tensors."""
+    import struct
+
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    out = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 1)
+    out += s("general.architecture") + struct.pack("<I", 8) + s(arch)
+    for name, dims, typ, off in tensors:
+        out += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        out += struct.pack("<IQ", typ, off)
+    out += b"\0" * ((-len(out)) % 32) + b"\0" * 64
+    return out
+
+
+def test_loader_rejects_overflowing_and_duplicate_tensors(tmp_path):
+    """Element counts and byte lengths are checked products (TensorInfo::byte_len, crates/gguf/src/lib.rs:
+    124-168): dims whose product wraps u64 fail instead of passing the end-of-file check; a repeated tensor
+    name is rejected."""
+    cases = {
+        "wrap": [("w", [1 << 33, 1 << 31], 0, 0)],              # 2^64 elements: wraps to 0
+        "bytes": [("w", [1 << 62, 2], 0, 0)],                   # 2^63 elements, 2^65 bytes
+        "dup": [("w", [16], 0, 0), ("w", [16], 0, 64)],
+    }
+    for name, ts in cases.items():
+        p = str(tmp_path / f"{name}.gguf")
+        open(p, "wb").write(_gguf_bytes(ts))
+        with pytest.raises(ribn_amd.RibnError) as e:
+            ribn_amd.QwenRocm(p)
+        assert e.value.code == -3, (name, e.value.message)
+        assert ("overflows" in e.value.message) if name != "dup" else ("duplicate tensor" in e.value.message)
