@@ -48,34 +48,53 @@ def algorithmic_bytes_per_token(info, ctx_mean, embd_row=None):
     return weights + norms + kv, weights
 
 
-def cpu_baseline(path, info):
-    """Oracle host dequant+matvec (restating dequantize_block + gguf_gemv) over layer 0 and the head."""
+def host_cpu():
+    """The host the CPU baselines run on: nproc, the cores this process may use, the CPU model, and the
+    thread count of the all-cores lines (capped at 16, the host share of one GPU on the GPU boxes)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"nproc": os.cpu_count(), "available": avail, "cpu_model": model, "threads_all": max(1, min(16, avail))}
+
+
+def cpu_baseline(path, info, host):
+    """The oracle's FP32 Qwen forward (restating qwen_reference.rs:368-556 with dequantize_block + gguf_gemv)
+    on the bench model itself: whole decode steps, every layer and the head, at positions 1 and 2 after one
+    untimed step. Single-threaded as the reference's host path, then with the matvec rows split over all
+    cores (bit-identical results)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import numpy as np
     import oracle_ffi as orc
-    g = orc.Gguf(path)
-    names = ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.attn_v.weight", "blk.0.attn_output.weight",
-             "blk.0.ffn_gate.weight", "blk.0.ffn_up.weight", "blk.0.ffn_down.weight", "output.weight"]
-    total_bytes, secs = 0, 0.0
-    rng = np.random.default_rng(0)
-    for n in names:
-        t, dims, _, data = g.tensor(n)
-        k, rows = dims
-        x = rng.standard_normal(k).astype(np.float32)
+    o = orc.QwenOracle(path, max_ctx=8)
+    o.set_threads(host["threads_all"])
+    o.step(1)                                   # untimed: pages the weights in
+    lines = {}
+    for label, threads, steps in (("one", 1, 2), ("all", host["threads_all"], 4)):
+        o.set_threads(threads)
         t0 = time.perf_counter()
-        orc.gemv(t, data, rows, k, x, threads=1)
-        secs += time.perf_counter() - t0
-        total_bytes += data.size
-    g.close()
-    gbs = total_bytes / secs / 1e9
-    weight_bytes = info.weight_bytes - info.vocab * (info.hidden // 256) * 144
-    return {"value": round(1.0 / (weight_bytes / (gbs * 1e9)), 4), "unit": "tok/s (extrapolated)", "cores": 1,
-            "kind": "port", "gbs": round(gbs, 3),
-            "sample": f"oracle dequant+matvec of blk.0 (7 matrices) + output.weight, {total_bytes / 1e6:.0f} MB, "
-                      f"{secs:.1f} s single-threaded; tok/s = host GB/s / weight bytes per token"}
+        for i in range(steps):
+            o.step(2 + i)
+        secs = (time.perf_counter() - t0) / steps
+        lines[label] = (1.0 / secs, secs)
+    o.close()
+    gb = info.weight_bytes / 1e9
+    one, allc = lines["one"], lines["all"]
+    return {"value": round(one[0], 4), "unit": "tok/s", "cores": 1, "kind": "port",
+            "gbs": round(gb / one[1], 3),
+            "sample": f"2 full decode steps of the bench model (36 layers + head, positions 2-3) through the C "
+                      f"oracle's FP32 forward, single-threaded: {one[1]:.2f} s per token",
+            "all_cores": {"value": round(allc[0], 4), "unit": "tok/s", "cores": host["threads_all"],
+                          "gbs": round(gb / allc[1], 3),
+                          "sample": "4 full decode steps, matvec rows split over the cores"},
+            "host": host}
 
 
-def gemma_cpu_baseline():
+def gemma_cpu_baseline(host=None):
     """the Gemma 4 host CPU BF16 decoder restatement (oracle/gemma4.c, restating
     crates/gemma4/src/cpu/) on the tiny random-init model, 64-token prompt then 32 greedy tokens,
     single-threaded as the reference's CPU path is."""
@@ -95,7 +114,25 @@ def gemma_cpu_baseline():
     t2 = time.perf_counter()
     d.close()
     decode_ms = (t2 - t1) * 1e3 / 31
+    threads = host["threads_all"] if host else 1
+    g4.set_threads(threads)
+    d = g4.Gemma4Oracle(c, w)
+    t3 = time.perf_counter()
+    lg2 = d.prefill(prompt)
+    t4 = time.perf_counter()
+    toks2 = [d.argmax(lg2)]
+    for _ in range(31):
+        toks2.append(d.argmax(d.decode(toks2[-1])))
+    t5 = time.perf_counter()
+    d.close()
+    g4.set_threads(1)
+    decode_ms_all = (t5 - t4) * 1e3 / 31
     return {"value": round(1e3 / decode_ms, 3), "unit": "tok/s (configs[0] decode)", "cores": 1, "kind": "port",
+            "all_cores": {"value": round(1e3 / decode_ms_all, 3), "cores": threads,
+                          "prefill_ms_per_token": round((t4 - t3) * 1e3 / 64, 3),
+                          "decode_ms_per_token": round(decode_ms_all, 3), "same_tokens": toks2 == toks,
+                          "sample": "same run with g4_project's outputs split over the cores"},
+            "host": host,
             "prefill_ms_per_token": round((t1 - t0) * 1e3 / 64, 3), "decode_ms_per_token": round(decode_ms, 3),
             "sample": "Gemma 4 CPU BF16 decoder restatement, tiny config (hidden 512, 4 layers, 8/2 heads x 64, "
                       "FFN 2048, vocab 32000), 64-token prompt + 32 greedy tokens, single-threaded",
@@ -398,8 +435,9 @@ def main():
             mr.generate(prompt, 2)
             toks_r, tmr = mr.generate(prompt, 2)
         prefill_res_tps = args.prompt / (tmr.prefill_ms / 1000.0)
-        cpu = None if args.no_cpu else cpu_baseline(path, info)
-        cpu_gemma = None if args.no_cpu else gemma_cpu_baseline()
+        host = host_cpu()
+        cpu = None if args.no_cpu else cpu_baseline(path, info, host)
+        cpu_gemma = None if args.no_cpu else gemma_cpu_baseline(host)
         gemma_gpu = gemma_rocm_line()
     finally:
         if made and os.path.exists(path):

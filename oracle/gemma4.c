@@ -8,6 +8,7 @@
 #include "gemma4.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -29,20 +30,57 @@ float g4_load(uint16_t bits) {
 
 static float bf16_f32(float v) { return g4_load(g4_bf16(v)); }
 
-/* project (cpu/linear.rs:23-66): out[r][c] = bf16(sum_k in[r][k] * w[c][k]), FP32 in k order */
-void g4_project(const uint16_t *input, int rows, int inner, const uint16_t *weight, int columns, uint16_t *out) {
-    for (int r = 0; r < rows; r++) {
-        const uint16_t *x = input + (size_t)r * inner;
-        for (int c = 0; c < columns; c++) {
-            const uint16_t *w = weight + (size_t)c * inner;
+/* Threads for g4_project (1 = the reference's single-threaded loops). Each
+ * output's sum is one sequential chain in one thread, so any thread count gives
+ * bit-identical results; the multi-threaded run is a CPU baseline line only. */
+static int g4_threads = 1;
+void g4_set_threads(int n) { g4_threads = n < 1 ? 1 : n > 64 ? 64 : n; }
+
+typedef struct {
+    const uint16_t *input, *weight;
+    uint16_t *out;
+    int rows, inner, columns, c0, c1;
+} g4_project_job;
+
+static void *g4_project_range(void *arg) {
+    const g4_project_job *j = (const g4_project_job *)arg;
+    for (int r = 0; r < j->rows; r++) {
+        const uint16_t *x = j->input + (size_t)r * j->inner;
+        for (int c = j->c0; c < j->c1; c++) {
+            const uint16_t *w = j->weight + (size_t)c * j->inner;
             float sum = 0.0f;
-            for (int k = 0; k < inner; k++) {
+            for (int k = 0; k < j->inner; k++) {
                 const float a = g4_load(x[k]), b = g4_load(w[k]);
                 sum += a * b;
             }
-            out[(size_t)r * columns + c] = g4_bf16(sum);
+            j->out[(size_t)r * j->columns + c] = g4_bf16(sum);
         }
     }
+    return NULL;
+}
+
+/* project (cpu/linear.rs:23-66): per output, an FP32 sum over k in order of
+ * separately rounded products, then one BF16 rounding */
+void g4_project(const uint16_t *input, int rows, int inner, const uint16_t *weight, int columns, uint16_t *out) {
+    int nt = g4_threads;
+    if (nt > columns) nt = columns;
+    if (nt <= 1) {
+        g4_project_job j = {input, weight, out, rows, inner, columns, 0, columns};
+        g4_project_range(&j);
+        return;
+    }
+    pthread_t th[64];
+    g4_project_job jobs[64];
+    const int per = (columns + nt - 1) / nt;
+    int started = 0;
+    for (int t = 0; t < nt; t++) {
+        const int c0 = t * per, c1 = c0 + per < columns ? c0 + per : columns;
+        jobs[t] = (g4_project_job){input, weight, out, rows, inner, columns, c0, c1};
+        if (c0 >= c1) continue;
+        if (pthread_create(&th[started], NULL, g4_project_range, &jobs[t]) != 0) g4_project_range(&jobs[t]);
+        else started++;
+    }
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
 }
 
 /* normalize (cpu/norm.rs:41-82): FP32 energy, (mean + eps)^-0.5, direct BF16 scale, one rounding */

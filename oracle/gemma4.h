@@ -55,6 +55,8 @@ typedef struct {
 uint16_t g4_bf16(float value);
 float g4_load(uint16_t bits);
 void g4_project(const uint16_t *input, int rows, int inner, const uint16_t *weight, int columns, uint16_t *out);
+/* worker threads of g4_project (default 1, the reference); results do not depend on it */
+void g4_set_threads(int n);
 /* scale == NULL: the scale-free value normalization */
 void g4_rms_norm(const uint16_t *input, int rows, int width, float eps, const uint16_t *scale, uint16_t *out);
 void g4_add(const uint16_t *a, const uint16_t *b, size_t n, uint16_t *out);

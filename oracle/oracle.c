@@ -491,6 +491,7 @@ struct orc_qwen {
     orc_layer *L;
     int pos_next;
     int kv_round;
+    int threads;   /* matvec worker threads (1 = the reference's host path); results do not depend on it */
 };
 
 static int get_tensor(orc_gguf *g, const char *name, uint32_t *type, const uint8_t **ptr,
@@ -656,13 +657,17 @@ static void kv_round(float *v, int n, int mode) {
     else if (mode == 2) for (int i = 0; i < n; i++) v[i] = orc_round_bf16(v[i]);
 }
 
+static int g_qwen_threads = 1;   /* set per call from the model being stepped */
 static void gemv(uint32_t t, const uint8_t *w, int rows, int k, const float *x, float *y) {
-    orc_gemv_q(t, w, (uint64_t)rows, (uint64_t)k, x, y, 1);
+    orc_gemv_q(t, w, (uint64_t)rows, (uint64_t)k, x, y, g_qwen_threads);
 }
+
+void orc_qwen_set_threads(orc_qwen *m, int threads) { m->threads = threads < 1 ? 1 : threads > 64 ? 64 : threads; }
 
 static int qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *trace, float *fnorm,
                      int kv_only) {
     if (pos != m->pos_next || pos >= m->max_ctx || (int)token >= m->vocab) return ORC_ERR_CONFIG;
+    g_qwen_threads = m->threads > 0 ? m->threads : 1;
     int H = m->hidden, hd = m->hd, qd = m->hq * hd, kd = m->hkv * hd, F = m->ffn;
     float *h = (float *)malloc(sizeof(float) * H), *xn = (float *)malloc(sizeof(float) * H);
     float *q = (float *)malloc(sizeof(float) * qd), *k = (float *)malloc(sizeof(float) * kd);

@@ -107,6 +107,10 @@ void orc_qwen_reset(orc_qwen *m);
  * 1 = binary16 RNE (the reference CUDA cache, model_ops.rs:1210-1276),
  * 2 = bfloat16 RNE (the build's default device cache). */
 void orc_qwen_set_kv_round(orc_qwen *m, int mode);
+/* Worker threads of the forward's matvecs (default 1, as the reference's host
+ * path). Rows are split between threads and each row's sum stays one sequential
+ * chain, so the results are bit-identical for every thread count. */
+void orc_qwen_set_threads(orc_qwen *m, int threads);
 float orc_round_f16(float x);
 float orc_round_bf16(float x);
 

@@ -63,6 +63,7 @@ def lib():
     L.g4_bf16.restype = c.c_uint16
     L.g4_bf16.argtypes = [c.c_float]
     L.g4_project.argtypes = [c.c_void_p, c.c_int, c.c_int, c.c_void_p, c.c_int, c.c_void_p]
+    L.g4_set_threads.argtypes = [c.c_int]
     L.g4_rms_norm.argtypes = [c.c_void_p, c.c_int, c.c_int, c.c_float, c.c_void_p, c.c_void_p]
     for f in (L.g4_add, L.g4_multiply):
         f.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_void_p]
@@ -85,6 +86,11 @@ def lib():
     L.g4_step.argtypes = [c.c_void_p, c.c_void_p, c.c_int, c.c_void_p]
     L._g4_ready = True
     return L
+
+
+def set_threads(n):
+    """Worker threads of g4_project (default 1, the reference's loops); results do not depend on it."""
+    lib().g4_set_threads(int(n))
 
 
 def ptr(a):

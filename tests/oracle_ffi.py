@@ -49,6 +49,7 @@ def lib():
         _lib.orc_qwen_append_kv.argtypes = [c.c_void_p, c.c_uint32, c.c_int]
         _lib.orc_qwen_reset.argtypes = [c.c_void_p]
         _lib.orc_qwen_set_kv_round.argtypes = [c.c_void_p, c.c_int]
+        _lib.orc_qwen_set_threads.argtypes = [c.c_void_p, c.c_int]
         _lib.orc_round_f16.restype = c.c_float
         _lib.orc_round_f16.argtypes = [c.c_float]
         _lib.orc_round_bf16.restype = c.c_float
@@ -176,6 +177,10 @@ class QwenOracle:
         assert rc == 0, rc
         self.pos += 1
         return logits, hid
+
+    def set_threads(self, n):
+        """Matvec worker threads (results are bit-identical for every count)."""
+        lib().orc_qwen_set_threads(self.h, int(n))
 
     def append_kv(self, token):
         """Advance one position, writing the K/V cache entries only (no readout)."""

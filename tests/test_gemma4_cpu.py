@@ -256,3 +256,18 @@ def test_configs0_tiny_gemma_greedy_is_deterministic():
     a = g4.Gemma4Oracle(c, w).generate(prompt, 8)
     b2 = g4.Gemma4Oracle(c, w).generate(prompt, 8)
     assert a == b2 and all(0 <= t < 32000 for t in a)
+
+
+def test_threaded_projection_is_bit_identical():
+    """The all-cores CPU baseline splits g4_project's outputs across threads; every logit stays identical."""
+    c = g4.config(vocab=512, hidden=128, intermediate=256, heads=4, kv_heads=2, head_dim=32, global_head_dim=32,
+                  ple=32, layers=("S", "F"))
+    w, keep = g4.synth_weights(c, seed=3)
+    prompt = [5, 9, 100, 7, 300]
+    ref = g4.Gemma4Oracle(c, w).prefill(prompt)
+    g4.set_threads(5)
+    try:
+        got = g4.Gemma4Oracle(c, w).prefill(prompt)
+    finally:
+        g4.set_threads(1)
+    assert np.array_equal(got, ref)

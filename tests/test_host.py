@@ -223,3 +223,18 @@ def test_loader_rejects_overflowing_and_duplicate_tensors(tmp_path):
             ribn_amd.QwenRocm(p)
         assert e.value.code == -3, (name, e.value.message)
         assert ("overflows" in e.value.message) if name != "dup" else ("duplicate tensor" in e.value.message)
+
+
+def test_oracle_threads_do_not_change_results(tmp_path):
+    """The oracle's multi-threaded matvecs (the all-cores CPU baseline) give bit-identical logits."""
+    p = str(tmp_path / "thr.gguf")
+    ribn_amd.synth_qwen_gguf(p, qwen3=True, hidden=256, layers=2, q_heads=4, kv_heads=2, head_dim=64, ffn=512,
+                             vocab=300, seed=17, norm_jitter=0.2, weight_std=0.05)
+    toks = [3, 77, 5, 120, 9]
+    out = []
+    for threads in (1, 7):
+        o = orc.QwenOracle(p, max_ctx=16)
+        o.set_threads(threads)
+        out.append(np.stack([o.step(t)[0] for t in toks]))
+        o.close()
+    assert np.array_equal(out[0], out[1])
