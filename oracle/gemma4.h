@@ -4,7 +4,13 @@
  *
  * Values are BF16 bit patterns (uint16_t). Every operation computes in FP32 and
  * rounds its result to BF16 once (round to nearest even), as the reference's
- * "eager" policy does; matrix products accumulate in FP32 in source order. */
+ * "eager" policy does; matrix products accumulate in FP32 in source order.
+ *
+ * Pinning: the operations by the reference's literal KATs (tests/cpu_ops.rs:21-135,
+ * cpu_attention.rs:22-92) and its rotary fixture bits; the composed decoder
+ * (g4_open/g4_step) by an independent numpy forward written from decoder.rs,
+ * bit-identical logits (tests/test_gemma_composition.py), and by the reference's
+ * prefill-equals-serial-decode invariant. */
 #ifndef RIBN_ORACLE_GEMMA4_H
 #define RIBN_ORACLE_GEMMA4_H
 

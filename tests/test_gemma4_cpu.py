@@ -10,12 +10,13 @@ reference's own known answers and by invariants (CPU only).
   crates/gemma4/tests/fixtures/rotary.json), within the reference test's 4-ULP
   budget (tests/rotary.rs:44-50), and against an FP64 evaluation of the same
   exponent.
-- Decoder composition: no golden logits exist in the reference for any small
-  model (its archived ones need the 14.9 GB E4B package), so the composed
-  decoder's absolute logits are parity unpinned. It is pinned by the reference's
-  own invariant: multi-row prefill equals serial decode bit for bit, across
-  sliding-window and shared-KV boundaries (cpu_prefill.rs:67-147). Rejected
-  chunks leave the continuation unchanged (cpu_prefill.rs:149-168).
+- Decoder composition: the reference holds no golden logits for any small model
+  (its archived ones need the 14.9 GB E4B package). The composed decoder is pinned
+  by an independent numpy forward written from decoder.rs (test_gemma_composition.py,
+  bit-identical logits) and, here, by the reference's own invariant: multi-row
+  prefill equals serial decode bit for bit, across sliding-window and shared-KV
+  boundaries (cpu_prefill.rs:67-147). Rejected chunks leave the continuation
+  unchanged (cpu_prefill.rs:149-168).
 """
 import json
 import os
