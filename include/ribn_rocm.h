@@ -301,6 +301,22 @@ typedef struct {
 } ribn_rocm_synth_config;
 int ribn_rocm_synth_qwen_gguf(const char *path, const ribn_rocm_synth_config *config, char *err,
                               size_t err_len);
+/* The hybrid fields of a synthetic qwen35 model (Gated-DeltaNet + gated
+ * attention, the reference's own architecture: crates/qwen/src/gguf/config.rs). */
+typedef struct {
+    uint32_t ssm_groups;      /* k heads of the recurrent layers (ssm.group_count) */
+    uint32_t ssm_heads;       /* v heads (ssm.time_step_rank), a multiple of ssm_groups */
+    uint32_t ssm_state;       /* head width of the recurrent layers (ssm.state_size) */
+    uint32_t conv_kernel;     /* 0 -> 4 */
+    uint32_t full_attention_interval;
+    uint32_t rope_dims;       /* rotated dims of the attention heads (0 -> head_dim) */
+    uint32_t ssm_type;        /* type of ssm_beta / ssm_alpha (0 -> Q8_0) */
+} ribn_rocm_synth_hybrid;
+/* Seeded synthetic qwen35 GGUF v3 (no reference counterpart: test inputs).
+ * `config` gives the shared geometry (hidden, layers, attention heads and
+ * head_dim, FFN, vocab, types, seed; rope_base 0 -> 1e7). */
+int ribn_rocm_synth_qwen35_gguf(const char *path, const ribn_rocm_synth_config *config,
+                                const ribn_rocm_synth_hybrid *hybrid, char *err, size_t err_len);
 /* Quantize n floats into GGML blocks (n a multiple of the block size). */
 int ribn_rocm_quantize(uint32_t type, const float *x, uint64_t n, uint8_t *out);
 

@@ -111,6 +111,21 @@ void orc_qwen_set_kv_round(orc_qwen *m, int mode);
  * path). Rows are split between threads and each row's sum stays one sequential
  * chain, so the results are bit-identical for every thread count. */
 void orc_qwen_set_threads(orc_qwen *m, int threads);
+/* ---- qwen35 hybrid forward (qwen35.c): Gated-DeltaNet + gated attention ---- */
+typedef struct orc_q35 orc_q35;
+int orc_q35_open(const char *gguf_path, int max_ctx, orc_q35 **out);
+void orc_q35_close(orc_q35 *m);
+/* hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, rot, ssm k heads,
+ * ssm v heads, ssm head width, full_attention_interval */
+void orc_q35_config(const orc_q35 *m, int32_t *cfg12);
+/* one token at `pos` (in order); logits and (layers+1)*hidden trace optional */
+int orc_q35_step(orc_q35 *m, uint32_t token, int pos, float *logits, float *hidden_trace);
+void orc_q35_reset(orc_q35 *m);
+void orc_q35_set_kv_round(orc_q35 *m, int mode);
+/* gdn_state_step on one head: state [kd][vd] (row = key index) updated in place,
+ * k, q [kd], v and out [vd] */
+void orc_gdn_state_step(float *state, const float *k, const float *v, const float *q, float decay, float beta,
+                        int kd, int vd, float *out);
 float orc_round_f16(float x);
 float orc_round_bf16(float x);
 

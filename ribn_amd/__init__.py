@@ -108,6 +108,12 @@ class SynthConfig(ctypes.Structure):
                 ("tied_output", ctypes.c_int32), ("threads", ctypes.c_int32)]
 
 
+class SynthHybrid(ctypes.Structure):
+    _fields_ = [("ssm_groups", ctypes.c_uint32), ("ssm_heads", ctypes.c_uint32), ("ssm_state", ctypes.c_uint32),
+                ("conv_kernel", ctypes.c_uint32), ("full_attention_interval", ctypes.c_uint32),
+                ("rope_dims", ctypes.c_uint32), ("ssm_type", ctypes.c_uint32)]
+
+
 def _sig(name, res, *args):
     f = getattr(_lib, name)
     f.restype = res
@@ -149,6 +155,8 @@ _sig("ribn_rocm_prefill_trace", _c.c_int, _c.c_void_p, _u32p, _c.c_uint32, _c.c_
 _sig("ribn_rocm_prefill_gemm", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f32p, _c.c_uint64, _f32p,
      _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_synth_qwen_gguf", _c.c_int, _c.c_char_p, _c.POINTER(SynthConfig), _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_synth_qwen35_gguf", _c.c_int, _c.c_char_p, _c.POINTER(SynthConfig), _c.POINTER(SynthHybrid), _c.c_char_p,
+     _c.c_size_t)
 _sig("ribn_rocm_quantize", _c.c_int, _c.c_uint32, _f32p, _c.c_uint64, _u8p)
 
 
@@ -180,6 +188,24 @@ def synth_qwen_gguf(path: str, *, qwen3: bool = True, hidden: int, layers: int, 
                       output_type, embd_type, int(tied_output), threads)
     err = ctypes.create_string_buffer(_ERR)
     _check(_lib.ribn_rocm_synth_qwen_gguf(path.encode(), ctypes.byref(cfg), err, _ERR), err)
+    return path
+
+
+def synth_qwen35_gguf(path: str, *, hidden: int, layers: int, q_heads: int, kv_heads: int, head_dim: int, ffn: int,
+                      vocab: int, ssm_groups: int, ssm_heads: int, ssm_state: int, full_attention_interval: int = 4,
+                      rope_dims: int = 0, conv_kernel: int = 4, ssm_type: int = GGML_Q8_0,
+                      weight_type: int = GGML_Q4_K, attn_v_type: int = 0, ffn_down_type: int = 0, output_type: int = 0,
+                      embd_type: int = 0, rope_base: float = 1e7, rms_eps: float = 1e-6, weight_std: float = 0.02,
+                      norm_jitter: float = 0.0, seed: int = 0, context_length: int = 32768, tied_output: bool = False,
+                      threads: int = 0) -> str:
+    """Write a seeded synthetic qwen35 hybrid GGUF v3 (Gated-DeltaNet recurrent layers, a gated full-attention
+    layer every `full_attention_interval` layers)."""
+    cfg = SynthConfig(1, hidden, layers, q_heads, kv_heads, head_dim, ffn, vocab, context_length, rope_base, rms_eps,
+                      weight_std, norm_jitter, seed, weight_type, attn_v_type, ffn_down_type, output_type, embd_type,
+                      int(tied_output), threads)
+    hy = SynthHybrid(ssm_groups, ssm_heads, ssm_state, conv_kernel, full_attention_interval, rope_dims, ssm_type)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_synth_qwen35_gguf(path.encode(), ctypes.byref(cfg), ctypes.byref(hy), err, _ERR), err)
     return path
 
 
@@ -501,7 +527,7 @@ class GemmaRocm:
 
 
 __all__ = [
-    "QwenRocm", "GemmaRocm", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
+    "QwenRocm", "GemmaRocm", "synth_qwen35_gguf", "BatchItem", "StepCompletion", "Admission", "RibnError", "synth_qwen_gguf", "quantize",
     "dequantize", "gemv", "bench_gemv", "prefill_gemm", "argmax", "LIB_PATH", "GGML_F32", "GGML_F16", "GGML_Q8_0", "GGML_Q4_K",
     "GGML_Q6_K", "BLOCK", "STEP_PREFILL", "STEP_DECODE", "ADMIT_READY", "ADMIT_REJECTED", "ADMIT_DEFERRED",
 ]

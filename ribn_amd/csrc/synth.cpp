@@ -130,6 +130,7 @@ struct TensorPlan {
     float stdev;   // for random tensors
     float fill;    // constant fill (norms) when stdev == 0
     uint64_t tid;
+    float jitter = -1.f;   // fill + N(0, jitter); < 0: the config's norm jitter for norm tensors
     uint64_t offset = 0;
     uint64_t bytes = 0;
 };
@@ -183,6 +184,57 @@ void encode_tensor(const TensorPlan& t, uint64_t seed, float jitter, uint8_t* ou
     for (auto& x : th) x.join();
 }
 
+// Lay out `plan`, write the header (metadata entries already encoded in
+// `kvs`, n_kv of them) and the tensor data.
+int write_gguf(const char* path, std::vector<TensorPlan>& plan, const std::vector<uint8_t>& kvs, uint64_t n_kv,
+               const ribn_rocm_synth_config* c, char* err, size_t err_len) {
+    uint64_t off = 0;
+    for (auto& t : plan) {
+        uint64_t be, bb;
+        if (!type_layout(t.type, &be, &bb) || t.dims[0] % be) {
+            set_err(err, err_len, "tensor " + t.name + ": type " + std::to_string(t.type) +
+                                      " does not fit dimension " + std::to_string(t.dims[0]));
+            return RIBN_ERR_INVALID;
+        }
+        uint64_t n = 1;
+        for (auto d : t.dims) n *= d;
+        t.bytes = n / be * bb;
+        t.offset = off;
+        off += (t.bytes + 31) / 32 * 32;
+    }
+    std::vector<uint8_t> hdr;
+    put_u32(hdr, 0x46554747u);
+    put_u32(hdr, 3);
+    put_u64(hdr, plan.size());
+    put_u64(hdr, n_kv);
+    hdr.insert(hdr.end(), kvs.begin(), kvs.end());
+    for (auto& t : plan) {
+        put_str(hdr, t.name);
+        put_u32(hdr, (uint32_t)t.dims.size());
+        for (auto d : t.dims) put_u64(hdr, d);
+        put_u32(hdr, t.type);
+        put_u64(hdr, t.offset);
+    }
+    while (hdr.size() % 32) hdr.push_back(0);
+    FILE* f = std::fopen(path, "wb");
+    if (!f) { set_err(err, err_len, std::string("cannot create ") + path); return RIBN_ERR_IO; }
+    bool ok = std::fwrite(hdr.data(), 1, hdr.size(), f) == hdr.size();
+    int threads = c->threads > 0 ? c->threads : (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<uint8_t> buf;
+    for (auto& t : plan) {
+        if (!ok) break;
+        uint64_t padded = (t.bytes + 31) / 32 * 32;
+        buf.assign(padded, 0);
+        const bool is_norm = t.name.find("norm") != std::string::npos;
+        const float jitter = t.jitter >= 0.f ? t.jitter : is_norm ? c->norm_jitter : 0.f;
+        encode_tensor(t, c->seed, jitter, buf.data(), threads);
+        ok = std::fwrite(buf.data(), 1, padded, f) == padded;
+    }
+    ok = (std::fclose(f) == 0) && ok;
+    if (!ok) { set_err(err, err_len, std::string("write failed: ") + path); return RIBN_ERR_IO; }
+    return RIBN_OK;
+}
+
 }  // namespace
 }  // namespace ribn
 
@@ -233,65 +285,106 @@ extern "C" int ribn_rocm_synth_qwen_gguf(const char* path, const ribn_rocm_synth
     add("output_norm.weight", {H}, GGML_F32, 0.f, 1.f);
     if (!c->tied_output) add("output.weight", {H, V}, ot, sd, 0.f);
 
-    uint64_t off = 0;
-    for (auto& t : plan) {
-        uint64_t be, bb;
-        if (!type_layout(t.type, &be, &bb) || t.dims[0] % be) {
-            set_err(err, err_len, "tensor " + t.name + ": type " + std::to_string(t.type) +
-                                      " does not fit dimension " + std::to_string(t.dims[0]));
-            return RIBN_ERR_INVALID;
+    std::vector<uint8_t> kvs;
+    kv_str(kvs, "general.architecture", arch);
+    kv_u32(kvs, "general.alignment", 32);
+    kv_str(kvs, "general.name", "ribn-rocm synthetic " + arch);
+    kv_u32(kvs, arch + ".context_length", c->context_length ? c->context_length : 32768);
+    kv_u32(kvs, arch + ".embedding_length", (uint32_t)H);
+    kv_u32(kvs, arch + ".block_count", (uint32_t)L);
+    kv_u32(kvs, arch + ".feed_forward_length", (uint32_t)F);
+    kv_u32(kvs, arch + ".attention.head_count", (uint32_t)hq);
+    kv_u32(kvs, arch + ".attention.head_count_kv", (uint32_t)hkv);
+    kv_u32(kvs, arch + ".attention.key_length", (uint32_t)hd);
+    kv_u32(kvs, arch + ".attention.value_length", (uint32_t)hd);
+    kv_f32(kvs, arch + ".rope.freq_base", c->rope_base > 0.f ? c->rope_base : 1e6f);
+    kv_f32(kvs, arch + ".attention.layer_norm_rms_epsilon", c->rms_eps > 0.f ? c->rms_eps : 1e-6f);
+    return write_gguf(path, plan, kvs, 13, c, err, err_len);
+}
+
+// qwen35 hybrid (Gated-DeltaNet recurrent layers + gated full attention): the
+// tensor names of crates/nvidia/src/decode.rs:52-82 and the metadata keys of
+// crates/qwen/src/gguf/config.rs:17-37. Layer i is full attention when (i + 1)
+// is a multiple of the interval. attn_q holds [q | gate] per head (2 * head_dim
+// rows each). ssm_a = -exp(A_log) is drawn negative, ssm_conv1d and the dt bias
+// from N(0, 0.3), the norms as 1 (+ jitter).
+extern "C" int ribn_rocm_synth_qwen35_gguf(const char* path, const ribn_rocm_synth_config* c,
+                                           const ribn_rocm_synth_hybrid* y, char* err, size_t err_len) {
+    if (!path || !c || !y) { set_err(err, err_len, "null argument"); return RIBN_ERR_INVALID; }
+    const uint64_t H = c->hidden, L = c->layers, hq = c->q_heads, hkv = c->kv_heads, hd = c->head_dim;
+    const uint64_t F = c->ffn, V = c->vocab, HK = y->ssm_groups, HV = y->ssm_heads, D = y->ssm_state;
+    const uint64_t KC = y->conv_kernel ? y->conv_kernel : 4, every = y->full_attention_interval;
+    if (!H || !L || !hq || !hkv || !hd || !F || !V || hq % hkv || !HK || !HV || !D || HV % HK || !every) {
+        set_err(err, err_len, "invalid synthetic hybrid geometry");
+        return RIBN_ERR_INVALID;
+    }
+    const uint64_t C = 2 * HK * D + HV * D, inner = HV * D;
+    const uint32_t def = c->weight_type ? c->weight_type : GGML_Q4_K;
+    const uint32_t vt = c->attn_v_type ? c->attn_v_type : def, dt = c->ffn_down_type ? c->ffn_down_type : def;
+    const uint32_t ot = c->output_type ? c->output_type : def, et = c->embd_type ? c->embd_type : def;
+    const uint32_t st = y->ssm_type ? y->ssm_type : GGML_Q8_0;
+    const float sd = c->weight_std > 0.f ? c->weight_std : 0.02f;
+    std::vector<TensorPlan> plan;
+    uint64_t tid = 1;
+    auto add = [&](const std::string& n, std::vector<uint64_t> dims, uint32_t t, float stdev, float fill,
+                   float jitter = -1.f) {
+        TensorPlan p{n, dims, t, stdev, fill, tid++};
+        p.jitter = jitter;
+        plan.push_back(p);
+    };
+    add("token_embd.weight", {H, V}, et, sd, 0.f);
+    for (uint64_t l = 0; l < L; l++) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        add(p + "attn_norm.weight", {H}, GGML_F32, 0.f, 1.f);
+        if ((l + 1) % every != 0) {
+            add(p + "attn_qkv.weight", {H, C}, def, sd, 0.f);
+            add(p + "attn_gate.weight", {H, inner}, def, sd, 0.f);
+            add(p + "ssm_beta.weight", {H, HV}, st, sd, 0.f);
+            add(p + "ssm_alpha.weight", {H, HV}, st, sd, 0.f);
+            add(p + "ssm_dt.bias", {HV}, GGML_F32, 0.3f, 0.f);
+            add(p + "ssm_a", {HV}, GGML_F32, 0.f, -1.f, 0.4f);
+            add(p + "ssm_conv1d.weight", {KC, C}, GGML_F32, 0.3f, 0.f);
+            add(p + "ssm_norm.weight", {D}, GGML_F32, 0.f, 1.f);
+            add(p + "ssm_out.weight", {inner, H}, def, sd, 0.f);
+        } else {
+            add(p + "attn_q.weight", {H, 2 * hq * hd}, def, sd, 0.f);
+            add(p + "attn_k.weight", {H, hkv * hd}, def, sd, 0.f);
+            add(p + "attn_v.weight", {H, hkv * hd}, vt, sd, 0.f);
+            add(p + "attn_q_norm.weight", {hd}, GGML_F32, 0.f, 1.f);
+            add(p + "attn_k_norm.weight", {hd}, GGML_F32, 0.f, 1.f);
+            add(p + "attn_output.weight", {hq * hd, H}, def, sd, 0.f);
         }
-        uint64_t n = 1;
-        for (auto d : t.dims) n *= d;
-        t.bytes = n / be * bb;
-        t.offset = off;
-        off += (t.bytes + 31) / 32 * 32;
+        add(p + "post_attention_norm.weight", {H}, GGML_F32, 0.f, 1.f);
+        add(p + "ffn_gate.weight", {H, F}, def, sd, 0.f);
+        add(p + "ffn_up.weight", {H, F}, def, sd, 0.f);
+        add(p + "ffn_down.weight", {F, H}, dt, sd, 0.f);
     }
-    std::vector<uint8_t> hdr;
-    put_u32(hdr, 0x46554747u);
-    put_u32(hdr, 3);
-    put_u64(hdr, plan.size());
-    const int n_kv = 13;
-    put_u64(hdr, n_kv);
-    kv_str(hdr, "general.architecture", arch);
-    kv_u32(hdr, "general.alignment", 32);
-    kv_str(hdr, "general.name", "ribn-rocm synthetic " + arch);
-    kv_u32(hdr, arch + ".context_length", c->context_length ? c->context_length : 32768);
-    kv_u32(hdr, arch + ".embedding_length", (uint32_t)H);
-    kv_u32(hdr, arch + ".block_count", (uint32_t)L);
-    kv_u32(hdr, arch + ".feed_forward_length", (uint32_t)F);
-    kv_u32(hdr, arch + ".attention.head_count", (uint32_t)hq);
-    kv_u32(hdr, arch + ".attention.head_count_kv", (uint32_t)hkv);
-    kv_u32(hdr, arch + ".attention.key_length", (uint32_t)hd);
-    kv_u32(hdr, arch + ".attention.value_length", (uint32_t)hd);
-    kv_f32(hdr, arch + ".rope.freq_base", c->rope_base > 0.f ? c->rope_base : 1e6f);
-    kv_f32(hdr, arch + ".attention.layer_norm_rms_epsilon", c->rms_eps > 0.f ? c->rms_eps : 1e-6f);
-    for (auto& t : plan) {
-        put_str(hdr, t.name);
-        put_u32(hdr, (uint32_t)t.dims.size());
-        for (auto d : t.dims) put_u64(hdr, d);
-        put_u32(hdr, t.type);
-        put_u64(hdr, t.offset);
-    }
-    while (hdr.size() % 32) hdr.push_back(0);
-    FILE* f = std::fopen(path, "wb");
-    if (!f) { set_err(err, err_len, std::string("cannot create ") + path); return RIBN_ERR_IO; }
-    bool ok = std::fwrite(hdr.data(), 1, hdr.size(), f) == hdr.size();
-    int threads = c->threads > 0 ? c->threads : (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-    std::vector<uint8_t> buf;
-    uint64_t written = 0;
-    for (auto& t : plan) {
-        if (!ok) break;
-        uint64_t padded = (t.bytes + 31) / 32 * 32;
-        buf.assign(padded, 0);
-        bool is_norm = t.name.find("norm") != std::string::npos;
-        encode_tensor(t, c->seed, is_norm ? c->norm_jitter : 0.f, buf.data(), threads);
-        ok = std::fwrite(buf.data(), 1, padded, f) == padded;
-        written += padded;
-    }
-    ok = (std::fclose(f) == 0) && ok;
-    if (!ok) { set_err(err, err_len, std::string("write failed: ") + path); return RIBN_ERR_IO; }
-    return RIBN_OK;
+    add("output_norm.weight", {H}, GGML_F32, 0.f, 1.f);
+    if (!c->tied_output) add("output.weight", {H, V}, ot, sd, 0.f);
+    const std::string a = "qwen35";
+    std::vector<uint8_t> kvs;
+    kv_str(kvs, "general.architecture", a);
+    kv_u32(kvs, "general.alignment", 32);
+    kv_str(kvs, "general.name", "ribn-rocm synthetic qwen35");
+    kv_u32(kvs, a + ".context_length", c->context_length ? c->context_length : 32768);
+    kv_u32(kvs, a + ".embedding_length", (uint32_t)H);
+    kv_u32(kvs, a + ".block_count", (uint32_t)L);
+    kv_u32(kvs, a + ".nextn_predict_layers", 0);
+    kv_u32(kvs, a + ".feed_forward_length", (uint32_t)F);
+    kv_u32(kvs, a + ".attention.head_count", (uint32_t)hq);
+    kv_u32(kvs, a + ".attention.head_count_kv", (uint32_t)hkv);
+    kv_u32(kvs, a + ".attention.key_length", (uint32_t)hd);
+    kv_u32(kvs, a + ".attention.value_length", (uint32_t)hd);
+    kv_f32(kvs, a + ".attention.layer_norm_rms_epsilon", c->rms_eps > 0.f ? c->rms_eps : 1e-6f);
+    kv_u32(kvs, a + ".rope.dimension_count", y->rope_dims ? y->rope_dims : (uint32_t)hd);
+    kv_f32(kvs, a + ".rope.freq_base", c->rope_base > 0.f ? c->rope_base : 1e7f);
+    kv_u32(kvs, a + ".full_attention_interval", (uint32_t)every);
+    kv_u32(kvs, a + ".ssm.group_count", (uint32_t)HK);
+    kv_u32(kvs, a + ".ssm.inner_size", (uint32_t)inner);
+    kv_u32(kvs, a + ".ssm.state_size", (uint32_t)D);
+    kv_u32(kvs, a + ".ssm.time_step_rank", (uint32_t)HV);
+    kv_u32(kvs, a + ".ssm.conv_kernel", (uint32_t)KC);
+    return write_gguf(path, plan, kvs, 21, c, err, err_len);
 }
 
 // Quantize `n` floats (a multiple of the block size) into GGML blocks.

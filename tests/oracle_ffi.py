@@ -50,6 +50,14 @@ def lib():
         _lib.orc_qwen_reset.argtypes = [c.c_void_p]
         _lib.orc_qwen_set_kv_round.argtypes = [c.c_void_p, c.c_int]
         _lib.orc_qwen_set_threads.argtypes = [c.c_void_p, c.c_int]
+        _lib.orc_q35_open.argtypes = [c.c_char_p, c.c_int, c.POINTER(c.c_void_p)]
+        _lib.orc_q35_close.argtypes = [c.c_void_p]
+        _lib.orc_q35_config.argtypes = [c.c_void_p, c.c_void_p]
+        _lib.orc_q35_step.argtypes = [c.c_void_p, c.c_uint32, c.c_int, c.c_void_p, c.c_void_p]
+        _lib.orc_q35_reset.argtypes = [c.c_void_p]
+        _lib.orc_q35_set_kv_round.argtypes = [c.c_void_p, c.c_int]
+        _lib.orc_gdn_state_step.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_void_p, c.c_float, c.c_float,
+                                            c.c_int, c.c_int, c.c_void_p]
         _lib.orc_round_f16.restype = c.c_float
         _lib.orc_round_f16.argtypes = [c.c_float]
         _lib.orc_round_bf16.restype = c.c_float
@@ -194,4 +202,49 @@ class QwenOracle:
     def close(self):
         if self.h:
             lib().orc_qwen_close(self.h)
+            self.h = None
+
+
+def gdn_state_step(state, k, v, q, decay, beta):
+    """The delta rule on one head (orc_gdn_state_step), state [key_dim][value_dim]: returns (new state, output)."""
+    st = np.ascontiguousarray(state, dtype=np.float32).copy()
+    kd, vd = st.shape
+    out = np.zeros(vd, dtype=np.float32)
+    arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (k, v, q)]
+    lib().orc_gdn_state_step(st.ctypes.data, arrs[0].ctypes.data, arrs[1].ctypes.data, arrs[2].ctypes.data,
+                             float(decay), float(beta), kd, vd, out.ctypes.data)
+    return st, out
+
+
+class Qwen35Oracle:
+    """FP32 qwen35 hybrid forward (oracle/qwen35.c)."""
+
+    def __init__(self, path, max_ctx=256, kv_round=0):
+        self.h = ctypes.c_void_p()
+        rc = lib().orc_q35_open(path.encode(), max_ctx, ctypes.byref(self.h))
+        if rc:
+            raise RuntimeError(f"qwen35 oracle open failed: {rc}")
+        lib().orc_q35_set_kv_round(self.h, kv_round)
+        cfg = (ctypes.c_int32 * 12)()
+        lib().orc_q35_config(self.h, cfg)
+        (self.hidden, self.layers, self.q_heads, self.kv_heads, self.head_dim, self.ffn, self.vocab, self.rot,
+         self.ssm_groups, self.ssm_heads, self.ssm_state, self.interval) = list(cfg)
+        self.pos = 0
+
+    def step(self, token, want_hidden=False):
+        logits = np.zeros(self.vocab, dtype=np.float32)
+        hid = np.zeros((self.layers + 1, self.hidden), dtype=np.float32) if want_hidden else None
+        rc = lib().orc_q35_step(self.h, int(token), self.pos, logits.ctypes.data,
+                                None if hid is None else hid.ctypes.data)
+        assert rc == 0, rc
+        self.pos += 1
+        return logits, hid
+
+    def reset(self):
+        lib().orc_q35_reset(self.h)
+        self.pos = 0
+
+    def close(self):
+        if self.h:
+            lib().orc_q35_close(self.h)
             self.h = None
