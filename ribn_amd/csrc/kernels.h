@@ -71,6 +71,7 @@ struct StepCtl {
     int32_t pos;
     int32_t pad;
     const int32_t* pages;
+    float* rec;          // hybrid models: the active sequence's recurrent state (else null)
 };
 
 enum MvMode : int32_t {
@@ -233,6 +234,31 @@ hipError_t launch_qk_rope_append(const PrefillRows& p, hipStream_t stream);
 hipError_t launch_prefill_attention(const PrefillRows& p, hipStream_t stream);
 hipError_t launch_silu_mul_f16(const float* gu, int f, int m, uint16_t* act, hipStream_t stream);
 hipError_t launch_set_pos(SeqState* s, int pos, hipStream_t stream);
+
+// Gated-DeltaNet block of a qwen35 hybrid layer (hybrid.hip), between the
+// segmented input matvec (mixed | z | beta_raw, alpha_raw) and ssm_out. Channel
+// layout of `mixed` / `act`: q heads [hk][d], k heads [hk][d], v heads [hv][d].
+// Recurrent state of the active sequence at ctl->rec: this layer's delta-rule
+// matrices at state_off ([hv][d rows = key][d cols = value]) and its
+// convolution history at conv_off ([channels][conv_k - 1], oldest first).
+struct GdnArgs {
+    const float* mixed;
+    const float* z;          // [hv][d]
+    const float* ba;         // [hv] beta_raw, then [hv] alpha_raw
+    const float* dt_bias;    // [hv]
+    const float* ssm_a;      // [hv], already -exp(A_log)
+    const float* conv_w;     // [channels][conv_k]
+    const float* ssm_norm;   // [d]
+    float* act;              // [channels]: conv + SiLU, q/k heads l2-normalized
+    float* gated;            // [hv][d] gated-norm output, ssm_out's input
+    const StepCtl* ctl;
+    size_t state_off, conv_off;
+    int hk, hv, d, conv_k;
+    float eps;
+};
+hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream);
+// x[i] *= sigmoid(gate[i]) (the gated full-attention output gate)
+hipError_t launch_gate_mul(float* x, const float* gate, int n, hipStream_t stream);
 
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);

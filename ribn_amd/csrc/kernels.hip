@@ -286,6 +286,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
         return hipErrorInvalidValue;
     if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
     if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
+    if (a.hd == 256) return a.kv_f16 ? attention_dispatch<256, true>(a, st) : attention_dispatch<256, false>(a, st);
     return hipErrorInvalidValue;
 }
 

@@ -30,6 +30,12 @@ namespace {
 
 struct Layer {
     QMat q, k, v, o, gate, up, down;
+    // qwen35 hybrid: a recurrent (Gated-DeltaNet) layer uses the gdn_* matrices and
+    // o = ssm_out; a gated full-attention layer adds the gate half of attn_q
+    bool recurrent = false;
+    QMat gdn_mix, gdn_z, gdn_ba, q_gate;
+    float *dt_bias = nullptr, *ssm_a = nullptr, *conv_w = nullptr, *ssm_norm = nullptr;
+    size_t state_off = 0, conv_off = 0;   // floats into a slot's recurrent state
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     float *q_bias = nullptr, *k_bias = nullptr, *v_bias = nullptr;
     uint16_t *kc = nullptr, *vc = nullptr;
@@ -78,6 +84,14 @@ struct ribn_rocm_model {
     uint64_t weight_bytes = 0, kv_bytes = 0;
 
     QMat embd{}, out{};
+    // qwen35 hybrid geometry (hybrid == false: dense qwen2/qwen3)
+    bool hybrid = false;
+    int ssm_hk = 0, ssm_hv = 0, ssm_d = 0, conv_k = 0, channels = 0, inner = 0, interval = 0;
+    float *mixed = nullptr, *zbuf = nullptr, *ba = nullptr, *gdn_act = nullptr, *gated = nullptr, *att_gate = nullptr;
+    float* d_rec = nullptr;          // [slots][rec_floats] recurrent state
+    size_t rec_floats = 0;
+    std::vector<MvArgs> mv_aux;      // gated attention: the gate projection
+    std::vector<int> wg_aux;
     uint16_t* w16_head = nullptr;   // resident binary16 output head
     BlasGemm* blas = nullptr;       // hipBLASLt state when the weights are resident
     float* out_norm = nullptr;
@@ -383,8 +397,33 @@ void build_launches(ribn_rocm_model* M) {
     hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, M->device);
     M->mv_qkv.clear(); M->mv_o.clear(); M->mv_gu.clear(); M->mv_down.clear();
     M->wg_qkv.clear(); M->wg_o.clear(); M->wg_gu.clear(); M->wg_down.clear();
+    M->mv_aux.clear(); M->wg_aux.clear();
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
+        M->mv_aux.push_back(MvArgs{});
+        M->wg_aux.push_back(0);
+        if (y.recurrent) {
+            // Gated-DeltaNet input: mix (q|k|v), z gate and beta|alpha in one launch
+            MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
+            q.waves = 8;
+            q.items_per_wave = one_pass_ipw((M->channels + M->inner + 2 * M->ssm_hv) / 2, q.waves, n_cu);
+            q.nseg = 3;
+            q.type_a = y.gdn_mix.type;
+            q.type_b = y.gdn_ba.type;
+            q.seg[0].w = y.gdn_mix; q.seg[0].out = M->mixed;
+            q.seg[1].w = y.gdn_z; q.seg[1].out = M->zbuf;
+            q.seg[2].w = y.gdn_ba; q.seg[2].out = M->ba;
+            M->wg_qkv.push_back(layout_segments(q));
+            M->mv_qkv.push_back(q);
+            MvArgs o = mv_base(M->gated, nullptr, 0.f, M->inner, MV_ADD, M->d_ctl);   // ssm_out + residual
+            o.nseg = 1;
+            o.seg[0].w = y.o; o.seg[0].out = M->h;
+            o.type_a = o.type_b = y.o.type;
+            o.waves = 8;
+            o.items_per_wave = one_pass_ipw(M->H / 2, o.waves, n_cu);
+            M->wg_o.push_back(layout_segments(o));
+            M->mv_o.push_back(o);
+        } else {
         MvArgs q = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
         q.waves = 8;
         q.items_per_wave = one_pass_ipw((qd + 2 * kd) / 2, q.waves, n_cu);
@@ -411,6 +450,17 @@ void build_launches(ribn_rocm_model* M) {
         o.items_per_wave = one_pass_ipw(M->H / 2, o.waves, n_cu);
         M->wg_o.push_back(layout_segments(o));
         M->mv_o.push_back(o);
+        if (M->hybrid) {   // gated attention: the gate half of attn_q, from the same normed input
+            MvArgs ga = mv_base(M->h, y.attn_norm, M->eps, M->H, MV_STORE, M->d_ctl);
+            ga.nseg = 1;
+            ga.seg[0].w = y.q_gate; ga.seg[0].out = M->att_gate;
+            ga.type_a = ga.type_b = y.q_gate.type;
+            ga.waves = 8;
+            ga.items_per_wave = one_pass_ipw(qd / 2, ga.waves, n_cu);
+            M->wg_aux.back() = layout_segments(ga);
+            M->mv_aux.back() = ga;
+        }
+        }
 
         MvArgs g = mv_base(M->h, y.ffn_norm, M->eps, M->H, MV_SILU, M->d_ctl);
         g.nseg = 1;
@@ -474,7 +524,7 @@ size_t align_floats(size_t n) { return (n + 63) / 64 * 64; }   // 256-byte sub-b
 // where every stage has its own buffer (see step.h).
 hipError_t build_step(ribn_rocm_model* M, bool allow) {
     M->step_wg = 0;
-    if (!allow) return hipSuccess;
+    if (!allow || M->hybrid) return hipSuccess;   // the persistent step has no recurrent stages
     const Layer& y0 = M->layers[0];
     StepKey key{(int)y0.q.type, (int)y0.v.type, (int)y0.o.type, (int)y0.gate.type, (int)y0.down.type,
                 (int)M->out.type, M->hd, M->hq / M->hkv, M->kv_f16 ? 1 : 0};
@@ -559,6 +609,17 @@ hipError_t build_step(ribn_rocm_model* M, bool allow) {
     return hipSuccess;
 }
 
+GdnArgs gdn_args(ribn_rocm_model* M, int l) {
+    const Layer& y = M->layers[l];
+    GdnArgs a{};
+    a.mixed = M->mixed; a.z = M->zbuf; a.ba = M->ba;
+    a.dt_bias = y.dt_bias; a.ssm_a = y.ssm_a; a.conv_w = y.conv_w; a.ssm_norm = y.ssm_norm;
+    a.act = M->gdn_act; a.gated = M->gated; a.ctl = M->d_ctl;
+    a.state_off = y.state_off; a.conv_off = y.conv_off;
+    a.hk = M->ssm_hk; a.hv = M->ssm_hv; a.d = M->ssm_d; a.conv_k = M->conv_k; a.eps = M->eps;
+    return a;
+}
+
 // One step of the token loop for the active sequence (decode.rs:550-640):
 // embedding (+rope table) -> L x [QKV(+norm) -> attention(+q/k norm, rope, KV
 // append) -> O(+residual) -> gate/up(+norm,+SwiGLU) -> down(+residual)]
@@ -579,9 +640,16 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
         return e;
     AttnArgs at = attn_args(M, 0, n_splits);
     for (int l = 0; l < M->L; l++) {
+        const Layer& y = M->layers[l];
         if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
-        at = attn_args(M, l, n_splits);
-        if ((e = launch_attention(at, st)) != hipSuccess) return e;
+        if (y.recurrent) {
+            if ((e = launch_gdn(gdn_args(M, l), st)) != hipSuccess) return e;
+        } else {
+            if (M->hybrid && (e = launch_matvec(M->mv_aux[l], M->wg_aux[l], st)) != hipSuccess) return e;
+            at = attn_args(M, l, n_splits);
+            if ((e = launch_attention(at, st)) != hipSuccess) return e;
+            if (M->hybrid && (e = launch_gate_mul(M->attn, M->att_gate, M->hq * M->hd, st)) != hipSuccess) return e;
+        }
         if ((e = launch_matvec(M->mv_o[l], M->wg_o[l], st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_down[l], M->wg_down[l], st)) != hipSuccess) return e;
@@ -823,7 +891,19 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
 
 // Prompt rows pos0 .. pos0 + n - 1 of the sequence in `slot` in chunks of at
 // most M->chunk rows; the last chunk samples the next token when `final`.
+hipError_t run_step(ribn_rocm_model* M, bool head, int ctx, float* trace);
+
 hipError_t prefill_rows(ribn_rocm_model* M, int slot, int pos0, int n, bool final) {
+    if (M->hybrid) {
+        // the recurrent layers advance one token at a time: prompt rows run as decode
+        // steps (the reference's default prefill lane; its chunk scan is opt-in,
+        // decode.rs gdn_chunk_scan), the last one sampling when `final`
+        for (int p = 0; p < n; p++) {
+            hipError_t e = run_step(M, final && p + 1 == n, pos0 + p + 1, nullptr);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     for (int p = 0; p < n; p += M->chunk) {
         const int m = std::min(M->chunk, n - p);
         hipError_t e = prefill_chunk(M, slot, pos0 + p, m, final && p + m == n, nullptr);
@@ -883,6 +963,9 @@ hipError_t reset_slot(ribn_rocm_model* M, int slot, const std::vector<int32_t>& 
         e = hipMemcpyAsync(M->d_tokens + (size_t)slot * (M->context + 1), ht, sizeof(uint32_t) * n_toks,
                            hipMemcpyHostToDevice, M->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(&M->d_slots[slot], &s, sizeof(SeqState), hipMemcpyHostToDevice, M->stream);
+    // a new sequence starts from a zero recurrent state (qwen35 hybrids)
+    if (e == hipSuccess && M->hybrid && M->rec_floats)
+        e = hipMemsetAsync(M->h_ctl[slot].rec, 0, sizeof(float) * M->rec_floats, M->stream);
     return e;
 }
 
@@ -959,13 +1042,14 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     if (!msg.empty()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
     std::string arch;
     if (!g.get_str("general.architecture", &arch)) { set_err(err, err_len, "missing general.architecture"); return RIBN_ERR_FORMAT; }
-    if (arch != "qwen2" && arch != "qwen3") {
-        set_err(err, err_len, "general.architecture `" + arch + "` is not supported (expected qwen2 or qwen3)");
+    if (arch != "qwen2" && arch != "qwen3" && arch != "qwen35") {
+        set_err(err, err_len, "general.architecture `" + arch + "` is not supported (expected qwen2, qwen3 or qwen35)");
         return RIBN_ERR_FORMAT;
     }
     std::unique_ptr<ribn_rocm_model, void (*)(ribn_rocm_model*)> Mp(new ribn_rocm_model(), ribn_rocm_free);
     ribn_rocm_model* M = Mp.get();
-    M->qwen3 = arch == "qwen3";
+    M->qwen3 = arch != "qwen2";
+    M->hybrid = arch == "qwen35";
     auto need_u = [&](const char* suffix, int* dst) -> bool {
         uint64_t v;
         if (!g.get_u64(arch + "." + suffix, &v) || v == 0 || v > (1u << 30)) {
@@ -987,13 +1071,50 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     if (g.get_u64(arch + ".attention.value_length", &vlen) && (int)vlen != M->hd) {
         set_err(err, err_len, arch + ".attention.value_length must equal key_length"); return RIBN_ERR_FORMAT;
     }
-    if ((M->hd != 64 && M->hd != 128) || M->rot > M->hd || M->rot % 2) {
-        set_err(err, err_len, arch + ".attention.key_length " + std::to_string(M->hd) + " is not supported (64 or 128)");
+    // head_dim 256 (the qwen35 27B's attention) runs the decode attention kernel only: hybrids have no
+    // chunked-prefill or batched-row attention
+    if ((M->hd != 64 && M->hd != 128 && !(M->hybrid && M->hd == 256)) || M->rot > M->hd || M->rot % 2) {
+        set_err(err, err_len, arch + ".attention.key_length " + std::to_string(M->hd) +
+                                  " is not supported (64 or 128; 256 for qwen35)");
         return RIBN_ERR_FORMAT;
     }
     if (M->hq % M->hkv || M->hq / M->hkv > 8) {
         set_err(err, err_len, arch + ".attention.head_count / head_count_kv must be an integer <= 8");
         return RIBN_ERR_FORMAT;
+    }
+    if (M->hybrid) {
+        // crates/qwen/src/gguf/config.rs:17-37 (keys) and :93-128 (periodic layer schedule)
+        if (!need_u("ssm.group_count", &M->ssm_hk) || !need_u("ssm.time_step_rank", &M->ssm_hv) ||
+            !need_u("ssm.state_size", &M->ssm_d) || !need_u("ssm.inner_size", &M->inner) ||
+            !need_u("ssm.conv_kernel", &M->conv_k))
+            return RIBN_ERR_FORMAT;
+        uint64_t nextn = 0;
+        if (g.get_u64("qwen35.nextn_predict_layers", &nextn) && nextn != 0) {
+            set_err(err, err_len, "qwen35.nextn_predict_layers: multi-token-prediction layers are not supported");
+            return RIBN_ERR_FORMAT;
+        }
+        if (g.get("qwen35.attention.recurrent_layers")) {
+            set_err(err, err_len, "qwen35.attention.recurrent_layers: only the periodic full_attention_interval "
+                                  "schedule is supported");
+            return RIBN_ERR_FORMAT;
+        }
+        uint64_t iv = 4;
+        g.get_u64("qwen35.full_attention_interval", &iv);
+        M->interval = (int)iv;
+        if (M->interval < 1 || M->interval > M->L) {
+            set_err(err, err_len, "qwen35.full_attention_interval must be in [1, block_count]"); return RIBN_ERR_FORMAT;
+        }
+        if ((M->ssm_d != 64 && M->ssm_d != 128) || M->ssm_hv % M->ssm_hk || M->inner != M->ssm_hv * M->ssm_d ||
+            M->conv_k < 2 || M->conv_k > 8) {
+            set_err(err, err_len, "qwen35.ssm: state_size must be 64 or 128, time_step_rank a multiple of group_count, "
+                                  "inner_size = time_step_rank * state_size, conv_kernel in [2, 8]");
+            return RIBN_ERR_FORMAT;
+        }
+        M->channels = 2 * M->ssm_hk * M->ssm_d + M->inner;
+        if (opts && (opts->flags & (RIBN_LOAD_RESIDENT_F16 | RIBN_LOAD_PERSISTENT_STEP))) {
+            set_err(err, err_len, "qwen35 hybrids run the default launch chain (no resident or persistent mode)");
+            return RIBN_ERR_INVALID;
+        }
     }
     if (M->H % 32 || M->F % 32 || M->H > 16384 || M->F > 28672) {
         set_err(err, err_len, arch + ".embedding_length and feed_forward_length must be multiples of 32 "
@@ -1065,9 +1186,23 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     else if ((rc = upload_mat(to, M->V, M->H, &M->out)) != RIBN_OK) return rc;
     if ((rc = upload_f32(ton, M->H, &M->out_norm)) != RIBN_OK) return rc;
     M->layers.resize(M->L);
+    size_t rec_off = 0;
     for (int l = 0; l < M->L; l++) {
         Layer& y = M->layers[l];
         auto T = [&](const char* nm) { return g.tensor("blk." + std::to_string(l) + "." + nm); };
+        auto lname = [&](const char* nm) { return "blk." + std::to_string(l) + "." + nm; };
+        auto mat = [&](const char* nm, uint64_t rows, uint64_t k, QMat* q) -> int {
+            const GgufTensor* t = T(nm);
+            const std::string full = lname(nm);
+            if ((msg = validate_type(t, full.c_str(), true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+            return upload_mat(t, rows, k, q);
+        };
+        auto vec = [&](const char* nm, uint64_t n, float** dst) -> int {
+            const GgufTensor* t = T(nm);
+            if (!t) { set_err(err, err_len, "missing tensor " + lname(nm)); return RIBN_ERR_FORMAT; }
+            return upload_f32(t, n, dst);
+        };
+        if (!M->hybrid) {
         struct { const char* n; uint64_t rows, k; QMat* q; } mats[] = {
             {"attn_q.weight", (uint64_t)qd, (uint64_t)M->H, &y.q},     {"attn_k.weight", (uint64_t)kd, (uint64_t)M->H, &y.k},
             {"attn_v.weight", (uint64_t)kd, (uint64_t)M->H, &y.v},     {"attn_output.weight", (uint64_t)M->H, (uint64_t)qd, &y.o},
@@ -1100,6 +1235,83 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             }
             if ((rc = upload_f32(t, vv.len, vv.dst)) != RIBN_OK) return rc;
         }
+        } else {
+            // qwen35 (decode.rs:52-82 tensor sets; config.rs:93-128 schedule)
+            y.recurrent = (l + 1) % M->interval != 0;
+            if ((rc = mat("ffn_gate.weight", M->F, M->H, &y.gate)) || (rc = mat("ffn_up.weight", M->F, M->H, &y.up)) ||
+                (rc = mat("ffn_down.weight", M->H, M->F, &y.down)) || (rc = vec("attn_norm.weight", M->H, &y.attn_norm)) ||
+                (rc = vec("post_attention_norm.weight", M->H, &y.ffn_norm)))
+                return rc;
+            if (y.gate.type != y.up.type) { set_err(err, err_len, "ffn_gate and ffn_up must share a value type"); return RIBN_ERR_FORMAT; }
+            if (y.recurrent) {
+                if ((rc = mat("attn_qkv.weight", M->channels, M->H, &y.gdn_mix)) ||
+                    (rc = mat("attn_gate.weight", M->inner, M->H, &y.gdn_z)) ||
+                    (rc = mat("ssm_out.weight", M->H, M->inner, &y.o)) || (rc = vec("ssm_dt.bias", M->ssm_hv, &y.dt_bias)) ||
+                    (rc = vec("ssm_a", M->ssm_hv, &y.ssm_a)) || (rc = vec("ssm_norm.weight", M->ssm_d, &y.ssm_norm)))
+                    return rc;
+                if (y.gdn_mix.type != y.gdn_z.type) {
+                    set_err(err, err_len, lname("attn_qkv.weight") + " and attn_gate.weight must share a value type");
+                    return RIBN_ERR_FORMAT;
+                }
+                // beta and alpha share one matrix of 2 * time_step_rank rows (beta first)
+                const GgufTensor* tb = T("ssm_beta.weight");
+                const GgufTensor* ta = T("ssm_alpha.weight");
+                const std::string nb = lname("ssm_beta.weight"), na = lname("ssm_alpha.weight");
+                if ((msg = validate_type(tb, nb.c_str(), true)).size() || (msg = validate_type(ta, na.c_str(), true)).size()) {
+                    set_err(err, err_len, msg); return RIBN_ERR_FORMAT;
+                }
+                if (tb->type != ta->type || tb->dims.size() != 2 || ta->dims.size() != 2 || tb->dims[0] != (uint64_t)M->H ||
+                    ta->dims[0] != (uint64_t)M->H || tb->dims[1] != (uint64_t)M->ssm_hv || ta->dims[1] != (uint64_t)M->ssm_hv) {
+                    set_err(err, err_len, nb + " and ssm_alpha.weight must be [embedding_length, time_step_rank] of one type");
+                    return RIBN_ERR_FORMAT;
+                }
+                {
+                    std::vector<uint8_t> cat(tb->bytes + ta->bytes);
+                    std::memcpy(cat.data(), g.data(*tb), tb->bytes);
+                    std::memcpy(cat.data() + tb->bytes, g.data(*ta), ta->bytes);
+                    HIPCHK(upload_qmat(M, tb->type, 2ull * M->ssm_hv, M->H, cat.data(), &y.gdn_ba, staging));
+                }
+                const GgufTensor* tc = T("ssm_conv1d.weight");
+                if (!tc || tc->type != GGML_F32 || tc->dims.size() != 2 || tc->dims[0] != (uint64_t)M->conv_k ||
+                    tc->dims[1] != (uint64_t)M->channels) {
+                    set_err(err, err_len, lname("ssm_conv1d.weight") + " must be F32 [conv_kernel, channels]");
+                    return RIBN_ERR_FORMAT;
+                }
+                HIPCHK(dalloc(M, &y.conv_w, tc->bytes));
+                HIPCHK(hipMemcpy(y.conv_w, g.data(*tc), tc->bytes, hipMemcpyHostToDevice));
+                y.state_off = rec_off;
+                rec_off += (size_t)M->ssm_hv * M->ssm_d * M->ssm_d;
+                y.conv_off = rec_off;
+                rec_off += (size_t)M->channels * (M->conv_k - 1);
+            } else {
+                // attn_q holds [q | gate] per head (2 head_dim rows each, qwen_reference.rs:379-385): split
+                // into a q matrix and a gate matrix so q|k|v feed the attention kernel as in dense layers
+                const GgufTensor* tq = T("attn_q.weight");
+                const std::string nq = lname("attn_q.weight");
+                if ((msg = validate_type(tq, nq.c_str(), true)).size()) { set_err(err, err_len, msg); return RIBN_ERR_FORMAT; }
+                if (tq->dims.size() != 2 || tq->dims[0] != (uint64_t)M->H || tq->dims[1] != 2ull * qd) {
+                    set_err(err, err_len, nq + " must be [embedding_length, 2 * head_count * key_length]");
+                    return RIBN_ERR_FORMAT;
+                }
+                uint64_t be, bb;
+                type_layout(tq->type, &be, &bb);
+                const size_t rb = (size_t)(M->H / be * bb), hb = rb * M->hd;
+                std::vector<uint8_t> qh((size_t)qd * rb), gh((size_t)qd * rb);
+                const uint8_t* src = g.data(*tq);
+                for (int h = 0; h < M->hq; h++) {
+                    std::memcpy(qh.data() + h * hb, src + (2 * h) * hb, hb);
+                    std::memcpy(gh.data() + h * hb, src + (2 * h + 1) * hb, hb);
+                }
+                HIPCHK(upload_qmat(M, tq->type, qd, M->H, qh.data(), &y.q, staging));
+                HIPCHK(upload_qmat(M, tq->type, qd, M->H, gh.data(), &y.q_gate, staging));
+                if ((rc = mat("attn_k.weight", kd, M->H, &y.k)) || (rc = mat("attn_v.weight", kd, M->H, &y.v)) ||
+                    (rc = mat("attn_output.weight", M->H, qd, &y.o)) || (rc = vec("attn_q_norm.weight", M->hd, &y.q_norm)) ||
+                    (rc = vec("attn_k_norm.weight", M->hd, &y.k_norm)))
+                    return rc;
+                if (y.q.type != y.k.type) { set_err(err, err_len, "attn_q and attn_k must share a value type"); return RIBN_ERR_FORMAT; }
+            }
+        }
+        if (y.recurrent) continue;
         const size_t kv_layer = (size_t)M->kv_pages * M->hkv * kPageTokens * M->hd;
         HIPCHK(dalloc(M, &y.kc, kv_layer * 2));
         HIPCHK(dalloc(M, &y.vc, kv_layer * 2));
@@ -1109,6 +1321,18 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     }
     staging.clear();
     staging.shrink_to_fit();
+    M->rec_floats = rec_off;
+    if (M->hybrid) {
+        HIPCHK(dalloc(M, &M->mixed, sizeof(float) * M->channels));
+        HIPCHK(dalloc(M, &M->gdn_act, sizeof(float) * M->channels));
+        HIPCHK(dalloc(M, &M->zbuf, sizeof(float) * M->inner));
+        HIPCHK(dalloc(M, &M->gated, sizeof(float) * M->inner));
+        HIPCHK(dalloc(M, &M->ba, sizeof(float) * 2 * M->ssm_hv));
+        HIPCHK(dalloc(M, &M->att_gate, sizeof(float) * qd));
+        const size_t slots_rec = (size_t)M->max_seqs + 1;
+        HIPCHK(dalloc(M, &M->d_rec, sizeof(float) * std::max<size_t>(1, slots_rec * M->rec_floats)));
+        HIPCHK(hipMemsetAsync(M->d_rec, 0, sizeof(float) * std::max<size_t>(1, slots_rec * M->rec_floats), M->stream));
+    }
 
     HIPCHK(dalloc(M, &M->h, sizeof(float) * M->H));
     HIPCHK(dalloc(M, &M->raw, sizeof(float) * (qd + 2 * kd)));
@@ -1148,7 +1372,8 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         M->p_part_floats = per_row * c;
         HIPCHK(dalloc(M, &M->p_part, sizeof(float) * M->p_part_floats));
         // batched decode rows: one per sequence, at most the chunk's rows
-        M->b_rows = (int)std::min<size_t>(c, M->max_seqs);
+        // (hybrids decode one sequence per step: the recurrent blocks have no batched form here)
+        M->b_rows = M->hybrid ? 0 : (int)std::min<size_t>(c, M->max_seqs);
         if (M->b_rows >= 2) {
             const size_t R = (size_t)M->b_rows;
             M->b_part_stride = (size_t)M->hkv * kMaxSplits * ((size_t)(M->hq / M->hkv) * M->hd + 2 * (M->hq / M->hkv));
@@ -1180,6 +1405,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         M->h_ctl[s].seq = &M->d_slots[s];
         M->h_ctl[s].pos = 0;
         M->h_ctl[s].pages = M->d_pages + (size_t)s * M->max_pages;
+        M->h_ctl[s].rec = M->hybrid ? M->d_rec + (size_t)s * M->rec_floats : nullptr;
         SeqState& st = M->h_state[s];
         st.pos = 0;
         st.last_token = 0;
@@ -1873,6 +2099,9 @@ extern "C" int ribn_rocm_prefill_trace(ribn_rocm_model* M, const uint32_t* token
     if (n == 0 || n + 1 > M->context) return fail(nullptr, err, err_len, "trace length outside the context", RIBN_ERR_INVALID);
     for (uint32_t i = 0; i < n; i++)
         if (tokens[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
+    if (M->hybrid)
+        return fail(nullptr, err, err_len, "qwen35 hybrids have no chunked prefill (prompt rows run as decode steps)",
+                    RIBN_ERR_INVALID);
     const int c = (int)std::max<uint32_t>(1, std::min<uint32_t>(chunk ? chunk : M->chunk, (uint32_t)M->chunk));
     std::vector<int32_t> pages;
     if (!take_pages(M, n + 1, &pages)) return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
