@@ -323,6 +323,54 @@ def run_config4(args):
     print(json.dumps(out))
 
 
+def run_qwen35(args):
+    """The reference's own architecture at its pinned geometry (crates/nvidia/src/qwen_reference.rs:10-21,
+    291-300, 488; 64 layers, a gated full-attention layer every 4th): hidden 5120, Gated-DeltaNet 16 k / 48 v
+    heads x 128 with a depth-4 convolution, gated attention 24 / 4 heads x 256 (64 rotated dims, base 1e7),
+    FFN 17408, Q4_K_M types, vocab 151936 (synthetic). Prompt rows run as decode steps; then greedy decode."""
+    import ribn_amd
+    import numpy as np
+    geo = dict(hidden=5120, layers=64, q_heads=24, kv_heads=4, head_dim=256, ffn=17408, vocab=151936,
+               ssm_groups=16, ssm_heads=48, ssm_state=128, full_attention_interval=4, rope_dims=64)
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_q35_{os.getpid()}.gguf")
+    t0 = time.time()
+    ribn_amd.synth_qwen35_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                               ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                               embd_type=ribn_amd.GGML_Q4_K, ssm_type=ribn_amd.GGML_Q8_0, **geo)
+    t_synth = time.time() - t0
+    n_prompt, n_new = 64, args.q35_tokens + 1
+    prompt = np.random.default_rng(0).integers(0, geo["vocab"], n_prompt).tolist()
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=n_prompt + n_new + 16, max_sequences=1) as m:
+            info = m.info
+            toks, tm = m.generate(prompt, n_new)
+    finally:
+        os.unlink(path)
+    steps = n_new - 1
+    ms = tm.decode_ms / steps
+    n_gdn = sum(1 for l in range(geo["layers"]) if (l + 1) % geo["full_attention_interval"])
+    state = n_gdn * (geo["ssm_heads"] * geo["ssm_state"] ** 2 + (2 * 16 + 48) * 128 * 3) * 4 * 2   # read + write
+    weights = info.weight_bytes - geo["vocab"] * (geo["hidden"] // 256) * 144 + geo["hidden"] // 256 * 144
+    kv = (geo["layers"] - n_gdn) * 2 * geo["kv_heads"] * geo["head_dim"] * 2 * (n_prompt + steps // 2)
+    step_bytes = weights + state + kv
+    out = {"metric": "qwen35 hybrid (Gated-DeltaNet + gated attention) 27B-geometry Q4_K_M decode tok/s @bs1",
+           "value": round(1e3 / ms, 2), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+           "ms_per_step": round(ms, 3), "dtype": "q4_k/q6_k/q8_0 weights x 16-bit fixed-point activations; FP32 "
+                                                 "recurrent state; f16 KV",
+           "step_hbm": {"bytes_per_token": int(step_bytes), "weight_bytes": int(weights),
+                        "recurrent_state_bytes": int(state),
+                        "achieved_gbs": round(step_bytes / (ms / 1e3) / 1e9, 1),
+                        "frac": round(step_bytes / (ms / 1e3) / 8e12, 4)},
+           "config": {"workload": "qwen35 27B geometry (the reference's pinned architecture)", "prompt": n_prompt,
+                      "decode_tokens": steps, **geo},
+           "reference_context": {"value": 32.3, "unit": "tok/s", "note": "the reference's own batch-1 decode of "
+                                 "Qwen3.8-27B UD-Q4_K_M (16.46 GB) on an RTX 4090, benchmarks/runtime-contract.md:1564; "
+                                 "other hardware and real weights, context only"},
+           "first_tokens": toks[:8].tolist(), "setup_s": {"synth": round(t_synth, 1)}}
+    print(json.dumps(out))
+
+
 def probe_traffic():
     """Launch sequence measured by the FETCH_SIZE / WRITE_SIZE passes: 20 replays each of the layer-0 gate/up,
     ffn_down and head matvecs (same kernels and shapes as the 36-layer model), then 5 copies of 1 GiB between
@@ -369,6 +417,8 @@ def main():
     ap.add_argument("--config", type=int, default=2,
                     help="2: the headline line (default); 1, 3 or 4: the configs[1] / [3] / [4] runs as their own line")
     ap.add_argument("--c3-tokens", type=int, default=256)
+    ap.add_argument("--q35", action="store_true", help="the qwen35 hybrid line at the reference's 27B geometry")
+    ap.add_argument("--q35-tokens", type=int, default=128)
     ap.add_argument("--c4-prompt", type=int, default=32768)
     ap.add_argument("--gemm", default="dequant", choices=["dequant", "resident"],
                     help="configs[3]/[4]: prefill / batched-decode GEMM path (resident = binary16 weight copies)")
@@ -386,6 +436,9 @@ def main():
 
     if args.probe_traffic:
         probe_traffic()
+        return
+    if args.q35:
+        run_qwen35(args)
         return
     if args.config == 1:
         run_config1(args)
