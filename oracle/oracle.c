@@ -492,6 +492,7 @@ struct orc_qwen {
     int pos_next;
     int kv_round;
     int threads;   /* matvec worker threads (1 = the reference's host path); results do not depend on it */
+    int intdot;    /* 1: projections in the integer-dot mode (Q8_1 activations) */
 };
 
 static int get_tensor(orc_gguf *g, const char *name, uint32_t *type, const uint8_t **ptr,
@@ -658,9 +659,23 @@ static void kv_round(float *v, int n, int mode) {
 }
 
 static int g_qwen_threads = 1;   /* set per call from the model being stepped */
+static int g_qwen_intdot = 0;
+/* One projection. In the integer-dot mode the input is packed to Q8_1 first and
+ * the projection runs on the packed words (CudaIntDotProjector::project,
+ * nvidia/src/decode.rs:1441-1497; every type of these models has an
+ * integer-dot kernel, so there is no float fallback here). */
 static void gemv(uint32_t t, const uint8_t *w, int rows, int k, const float *x, float *y) {
+    if (g_qwen_intdot && (t == 8 || t == 12 || t == 14)) {
+        uint32_t *pk = (uint32_t *)malloc(sizeof(uint32_t) * (size_t)(k / 32) * 9);
+        orc_quantize_q8_1(x, (uint64_t)k, pk);
+        orc_gemv_q8_1(t, w, (uint64_t)rows, (uint64_t)k, pk, 1, y, g_qwen_threads);
+        free(pk);
+        return;
+    }
     orc_gemv_q(t, w, (uint64_t)rows, (uint64_t)k, x, y, g_qwen_threads);
 }
+
+void orc_qwen_set_gemv_mode(orc_qwen *m, int mode) { m->intdot = mode == ORC_GEMV_INT_DOT; }
 
 void orc_qwen_set_threads(orc_qwen *m, int threads) { m->threads = threads < 1 ? 1 : threads > 64 ? 64 : threads; }
 
@@ -668,6 +683,7 @@ static int qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float 
                      int kv_only) {
     if (pos != m->pos_next || pos >= m->max_ctx || (int)token >= m->vocab) return ORC_ERR_CONFIG;
     g_qwen_threads = m->threads > 0 ? m->threads : 1;
+    g_qwen_intdot = m->intdot;
     int H = m->hidden, hd = m->hd, qd = m->hq * hd, kd = m->hkv * hd, F = m->ffn;
     float *h = (float *)malloc(sizeof(float) * H), *xn = (float *)malloc(sizeof(float) * H);
     float *q = (float *)malloc(sizeof(float) * qd), *k = (float *)malloc(sizeof(float) * kd);
@@ -758,4 +774,152 @@ int orc_qwen_step(orc_qwen *m, uint32_t token, int pos, float *logits, float *tr
 
 int orc_qwen_append_kv(orc_qwen *m, uint32_t token, int pos) {
     return qwen_step(m, token, pos, NULL, NULL, NULL, 1);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Integer-dot projections: the reference's experimental GemvMode::IntegerDot
+ * (nvidia/src/decode.rs:298-312), lossy by design. */
+
+/* Bits of a value already representable in binary16 (finite, or +-inf). */
+static uint16_t f16_bits(float r) {
+    uint32_t u;
+    memcpy(&u, &r, 4);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    float a = fabsf(r);
+    if (a == 0.0f) return sign;
+    if (isinf(a)) return (uint16_t)(sign | 0x7c00u);
+    if (a < ldexpf(1.0f, -14)) return (uint16_t)(sign | (uint16_t)(a * 16777216.0f));
+    int e;
+    float f = frexpf(a, &e);   /* a = f 2^e, f in [0.5, 1) */
+    uint16_t mant = (uint16_t)((f * 2.0f - 1.0f) * 1024.0f);
+    return (uint16_t)(sign | (uint16_t)((e - 1 + 15) << 10) | mant);
+}
+
+/* quantize_q8_1 (nvidia/src/activation.cu:1-28): per 32 values, d = max|x| /
+ * 127, q = round-half-away(x / d) (0 when the block is all zero), word 0 =
+ * half(d) | half(sum) << 16 (round to nearest even), words 1..8 = q as signed
+ * bytes, little endian. The sum follows the warp's xor butterfly (offsets 16,
+ * 8, 4, 2, 1): lane 0 ends with ((..(x0 + x16) + (x8 + x24)) ..). */
+int orc_quantize_q8_1(const float *x, uint64_t n, uint32_t *out) {
+    if (n == 0 || n % 32) return ORC_ERR_DIMENSION;
+    for (uint64_t b = 0; b < n / 32; b++) {
+        const float *v = x + b * 32;
+        float s[32], mx = 0.0f;
+        for (int i = 0; i < 32; i++) { s[i] = v[i]; mx = fmaxf(mx, fabsf(v[i])); }
+        for (int off = 16; off > 0; off >>= 1)
+            for (int i = 0; i < off; i++) s[i] = s[i] + s[i + off];
+        const float d = mx / 127.0f;
+        uint32_t *w = out + b * 9;
+        w[0] = (uint32_t)f16_bits(orc_round_f16(d)) | ((uint32_t)f16_bits(orc_round_f16(s[0])) << 16);
+        for (int j = 0; j < 8; j++) {
+            uint32_t word = 0;
+            for (int i = 0; i < 4; i++) {
+                const int q = mx == 0.0f ? 0 : (int)roundf(v[4 * j + i] / d);
+                word |= ((uint32_t)q & 0xffu) << (8 * i);
+            }
+            w[1 + j] = word;
+        }
+    }
+    return ORC_OK;
+}
+
+/* One output of the integer-dot matvec for one packed input (`nb` blocks of
+ * the row, `act` = K/32 nine-word Q8_1 blocks), in exact binary64 arithmetic:
+ * the value every kernel ordering approximates.
+ *   Q4_K (q4_k_q8_1.cu:40-81):  sum_g (d sc_g) da_g dot_g - (dmin m_g) S_g
+ *   Q6_K (q6_k_q8_1.cu:37-90):  sum_h (d sc_h) da dot(q6 + 32 ... ) with the
+ *                               bias removed through the packed byte sums,
+ *                               i.e. sum_h (d sc_h) da (dot_h - 32 A_h)
+ *   Q8_0 (q8_0_q8_1.cu:27-55):  sum_b d_b da_b dot_b
+ * with da, S the half-precision scale and sum of the Q8_1 block. */
+static double intdot_row(uint32_t t, const uint8_t *row, uint64_t k, const uint32_t *act) {
+    double acc = 0.0;
+    if (t == 8) {
+        for (uint64_t b = 0; b < k / 32; b++) {
+            const uint8_t *e = row + b * 34;
+            const uint32_t *a = act + b * 9;
+            int dot = 0;
+            for (int i = 0; i < 32; i++) dot += (int)(int8_t)e[2 + i] * (int)(int8_t)(a[1 + i / 4] >> (8 * (i % 4)));
+            acc += (double)rd_f16(e) * (double)orc_f16_to_f32((uint16_t)a[0]) * (double)dot;
+        }
+        return acc;
+    }
+    for (uint64_t b = 0; b < k / 256; b++) {
+        if (t == 12) {
+            const uint8_t *e = row + b * 144;
+            const double d = rd_f16(e), dmin = rd_f16(e + 2);
+            uint8_t sc[8], mn[8];
+            q4k_scales(e + 4, sc, mn);
+            for (int g = 0; g < 8; g++) {
+                const uint32_t *a = act + (b * 8 + (uint64_t)g) * 9;
+                int dot = 0;
+                for (int i = 0; i < 32; i++) {
+                    const int q = (e[16 + (g / 2) * 32 + i] >> ((g % 2) * 4)) & 15;
+                    dot += q * (int)(int8_t)(a[1 + i / 4] >> (8 * (i % 4)));
+                }
+                const double da = orc_f16_to_f32((uint16_t)a[0]), S = orc_f16_to_f32((uint16_t)(a[0] >> 16));
+                acc += d * sc[g] * da * (double)dot - dmin * mn[g] * S;
+            }
+        } else {
+            const uint8_t *e = row + b * 210;
+            const double d = rd_f16(e + 208);
+            for (int g = 0; g < 8; g++) {
+                const uint32_t *a = act + (b * 8 + (uint64_t)g) * 9;
+                const double da = orc_f16_to_f32((uint16_t)a[0]);
+                const int chunk = g / 4, variant = g % 4;
+                for (int half = 0; half < 2; half++) {
+                    int dot = 0, asum = 0;
+                    for (int i = 0; i < 16; i++) {
+                        const int pos = half * 16 + i;
+                        const int lo = (e[chunk * 64 + (variant % 2) * 32 + pos] >> (variant < 2 ? 0 : 4)) & 15;
+                        const int hi = (e[128 + chunk * 32 + pos] >> (2 * variant)) & 3;
+                        const int qa = (int)(int8_t)(a[1 + pos / 4] >> (8 * (pos % 4)));
+                        dot += (lo | (hi << 4)) * qa;
+                        asum += qa;
+                    }
+                    acc += d * (double)(int8_t)e[192 + g * 2 + half] * da * (double)(dot - 32 * asum);
+                }
+            }
+        }
+    }
+    return acc;
+}
+
+typedef struct {
+    uint32_t t; const uint8_t *w; uint64_t k, rows, r0, r1, row_bytes; const uint32_t *pk; uint32_t members; float *y;
+} intdot_job;
+
+static void *intdot_worker(void *arg) {
+    intdot_job *j = (intdot_job *)arg;
+    for (uint32_t m = 0; m < j->members; m++)
+        for (uint64_t n = j->r0; n < j->r1; n++)
+            j->y[(uint64_t)m * j->rows + n] =
+                (float)intdot_row(j->t, j->w + n * j->row_bytes, j->k, j->pk + (uint64_t)m * (j->k / 32) * 9);
+    return NULL;
+}
+
+/* y[m][n] for `members` packed inputs (batch-major, K/32 * 9 words each), the
+ * batched variant reading each weight row once for every member
+ * (q4_k_q8_1_gemv_batch, q4_k_q8_1.cu:86-140). */
+int orc_gemv_q8_1(uint32_t t, const uint8_t *w, uint64_t rows, uint64_t k, const uint32_t *packed,
+                  uint32_t members, float *y, int threads) {
+    uint64_t be, bb;
+    if (t != 8 && t != 12 && t != 14) return ORC_ERR_UNSUPPORTED_TYPE;
+    orc_tensor_layout(t, &be, &bb);
+    if (k == 0 || k % be || members == 0) return ORC_ERR_DIMENSION;
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    intdot_job jobs[64];
+    pthread_t th[64];
+    uint64_t per = (rows + (uint64_t)threads - 1) / (uint64_t)threads;
+    for (int i = 0; i < threads; i++) {
+        uint64_t r0 = per * (uint64_t)i, r1 = r0 + per;
+        if (r0 > rows) r0 = rows;
+        if (r1 > rows) r1 = rows;
+        jobs[i] = (intdot_job){t, w, k, rows, r0, r1, (k / be) * bb, packed, members, y};
+        if (threads == 1) intdot_worker(&jobs[i]);
+        else pthread_create(&th[i], NULL, intdot_worker, &jobs[i]);
+    }
+    if (threads > 1) for (int i = 0; i < threads; i++) pthread_join(th[i], NULL);
+    return ORC_OK;
 }

@@ -17,6 +17,15 @@
  *   orc_rms_norm          pinned: constant-vector closed form
  *   orc_rope_neox         pinned: pos 0 identity, norm preservation, pos-additivity
  *   orc_argmax            pinned: ties -> lowest index, NaN skipped
+ *   orc_quantize_q8_1     pinned: reference KAT (nvidia/tests/cuda_activation.rs:8-44),
+ *                         dyadic inputs packed without loss (q4_q8_1.rs:88-101,
+ *                         200-222), |x - d q| <= d/2 and the header sum within
+ *                         half rounding of the exact sum
+ *   orc_gemv_q8_1         pinned: the reference's host fixtures and bounds
+ *                         (q4_q8_1.rs, q6_q8_1.rs, q8_0_q8_1.rs: exact on dyadic
+ *                         inputs, within the packing error bound of the float
+ *                         product otherwise) and a brute force over dequantized
+ *                         weights and dequantized Q8_1 activations
  *   orc_qwen_*            composition of the above; the reference cannot run dense
  *                         Qwen2/Qwen3, so the composed forward is pinned only by
  *                         its parts plus single-token closed forms (1-token
@@ -111,6 +120,10 @@ void orc_qwen_set_kv_round(orc_qwen *m, int mode);
  * path). Rows are split between threads and each row's sum stays one sequential
  * chain, so the results are bit-identical for every thread count. */
 void orc_qwen_set_threads(orc_qwen *m, int threads);
+/* Projection mode of later steps: ORC_GEMV_FLOAT (default) or ORC_GEMV_INT_DOT,
+ * the reference's GemvMode::IntegerDot (nvidia/src/decode.rs:298-312). */
+enum { ORC_GEMV_FLOAT = 0, ORC_GEMV_INT_DOT = 2 };
+void orc_qwen_set_gemv_mode(orc_qwen *m, int mode);
 /* ---- qwen35 hybrid forward (qwen35.c): Gated-DeltaNet + gated attention ---- */
 typedef struct orc_q35 orc_q35;
 int orc_q35_open(const char *gguf_path, int max_ctx, orc_q35 **out);
@@ -127,6 +140,12 @@ void orc_q35_set_kv_round(orc_q35 *m, int mode);
 void orc_gdn_state_step(float *state, const float *k, const float *v, const float *q, float decay, float beta,
                         int kd, int vd, float *out);
 float orc_round_f16(float x);
+/* quantize_q8_1 (nvidia/src/activation.cu): n % 32 == 0, out gets n/32 * 9 words. */
+int orc_quantize_q8_1(const float *x, uint64_t n, uint32_t *out);
+/* Integer-dot matvec over Q8_1-packed inputs (types Q8_0, Q4_K, Q6_K); `packed`
+ * holds `members` inputs of k/32 * 9 words, y gets [members][rows]. */
+int orc_gemv_q8_1(uint32_t value_type, const uint8_t *w, uint64_t rows, uint64_t k, const uint32_t *packed,
+                  uint32_t members, float *y, int threads);
 float orc_round_bf16(float x);
 
 #ifdef __cplusplus

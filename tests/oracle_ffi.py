@@ -62,6 +62,10 @@ def lib():
         _lib.orc_round_f16.argtypes = [c.c_float]
         _lib.orc_round_bf16.restype = c.c_float
         _lib.orc_round_bf16.argtypes = [c.c_float]
+        _lib.orc_quantize_q8_1.argtypes = [c.c_void_p, c.c_uint64, c.c_void_p]
+        _lib.orc_gemv_q8_1.argtypes = [c.c_uint32, c.c_void_p, c.c_uint64, c.c_uint64, c.c_void_p, c.c_uint32,
+                                       c.c_void_p, c.c_int]
+        _lib.orc_qwen_set_gemv_mode.argtypes = [c.c_void_p, c.c_int]
     return _lib
 
 
@@ -103,6 +107,28 @@ def gemv(t, blocks, rows, k, x, threads=1):
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.zeros(rows, dtype=np.float32)
     assert lib().orc_gemv_q(t, blocks.ctypes.data, rows, k, x.ctypes.data, y.ctypes.data, threads) == 0
+    return y
+
+
+def quantize_q8_1(x):
+    """Q8_1 words (n/32 blocks of 9 u32) of a float vector (orc_quantize_q8_1)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size // 32 * 9, dtype=np.uint32)
+    rc = lib().orc_quantize_q8_1(x.ctypes.data, x.size, out.ctypes.data)
+    if rc:
+        raise ValueError(f"orc_quantize_q8_1: {rc}")
+    return out
+
+
+def gemv_q8_1(t, blocks, rows, k, packed, members=1, threads=1):
+    """Integer-dot matvec over Q8_1 inputs: y [members][rows] (orc_gemv_q8_1)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    assert packed.size == members * (k // 32) * 9
+    y = np.zeros((members, rows), dtype=np.float32)
+    rc = lib().orc_gemv_q8_1(t, blocks.ctypes.data, rows, k, packed.ctypes.data, members, y.ctypes.data, threads)
+    if rc:
+        raise ValueError(f"orc_gemv_q8_1: {rc}")
     return y
 
 
@@ -189,6 +215,12 @@ class QwenOracle:
     def set_threads(self, n):
         """Matvec worker threads (results are bit-identical for every count)."""
         lib().orc_qwen_set_threads(self.h, int(n))
+
+    GEMV_FLOAT, GEMV_INT_DOT = 0, 2
+
+    def set_gemv_mode(self, mode):
+        """Projection mode of the following steps (GEMV_INT_DOT: Q8_1 activations, integer dots)."""
+        lib().orc_qwen_set_gemv_mode(self.h, int(mode))
 
     def append_kv(self, token):
         """Advance one position, writing the K/V cache entries only (no readout)."""
