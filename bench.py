@@ -194,7 +194,7 @@ def run_config3(args):
     prompts = [rng.integers(0, CFG["vocab"], int(n)).tolist() for n in rng.integers(256, 2049, n_seq)]
     try:
         with ribn_amd.QwenRocm(path, context_tokens=2048 + n_out + 16, max_sequences=n_seq,
-                               max_batch_tokens=budget, kv="bf16", gemm=args.gemm) as m:
+                               max_batch_tokens=budget, kv="bf16", gemm=args.gemm, gemv=args.gemv) as m:
             seqs = {}
             for i, p in enumerate(prompts):
                 a = m.admit(1000 + i, i + 1, p, n_out)
@@ -250,10 +250,15 @@ def run_config3(args):
            "decode_phase_tok_s": round(decode_after / max(1e-9, t0 + wall - t_all_prefilled), 1)
            if t_all_prefilled else None,
            "median_first_token_s": round(float(np.median(first_token_s)), 2),
-           "config": {"workload": "BASELINE configs[3]", "kv": "bf16 paged, 16-token pages", "gemm": args.gemm, "sequences": n_seq, "prompt": "U[256,2048]",
+           "config": {"workload": "BASELINE configs[3]", "kv": "bf16 paged, 16-token pages", "gemm": args.gemm,
+                      "gemv": args.gemv, "sequences": n_seq, "prompt": "U[256,2048]",
                       "chunk": chunk, "batch_token_budget": budget, "decode_tokens": n_out},
-           "note": "a batch's decode rows run as one batched step through the MFMA GEMMs (per-row split-K "
-                   "attention over each sequence's pages); prefill rows run chunked MFMA prefill"}
+           "note": ("a batch's decode rows run as one batched step through the MFMA GEMMs (per-row split-K "
+                    "attention over each sequence's pages); prefill rows run chunked MFMA prefill")
+           if args.gemv == "float" else
+                   ("integer-dot mode (the reference's lossy GemvMode::IntegerDot): a batch's decode rows run as "
+                    "one batched step whose projections pack their inputs to Q8_1 and read the weights once per "
+                    "group of 8 rows (v_dot4_i32_i8); prefill rows run chunked MFMA prefill")}
     print(json.dumps(out))
 
 
@@ -422,6 +427,8 @@ def main():
     ap.add_argument("--c4-prompt", type=int, default=32768)
     ap.add_argument("--gemm", default="dequant", choices=["dequant", "resident"],
                     help="configs[3]/[4]: prefill / batched-decode GEMM path (resident = binary16 weight copies)")
+    ap.add_argument("--gemv", default="float", choices=["float", "int-dot"],
+                    help="configs[3]: decode-row projections (int-dot = the reference's lossy GemvMode::IntegerDot)")
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: replays the gate/up, down and head "

@@ -77,6 +77,16 @@ typedef struct {
  * batch-1 decode matvecs keep streaming the GGUF planes. libhipblaslt.so is
  * opened at load only when this flag is set (RIBN_ERR_DEVICE if it cannot be). */
 #define RIBN_LOAD_RESIDENT_F16 4u
+/* Integer-dot decode projections, the reference's experimental, lossy
+ * GemvMode::IntegerDot (nvidia/src/decode.rs:298-312, CudaIntDotProjector
+ * decode.rs:1409-1553): every sampled decode row (batched rows of several
+ * sequences and single steps alike) packs each projection input to Q8_1
+ * (quantize_q8_1, nvidia/src/activation.cu) and runs the integer-dot matvec
+ * (q4_k_q8_1.cu, q6_k_q8_1.cu, q8_0_q8_1.cu; weights read once for up to 8 rows).
+ * Prompt rows keep the float path. Not token-identical to the default mode. Not
+ * with RIBN_LOAD_PERSISTENT_STEP or qwen35 hybrids; ribn_rocm_trace and
+ * ribn_rocm_prefill_trace refuse such a model. */
+#define RIBN_LOAD_INT_DOT 8u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);
@@ -219,6 +229,19 @@ int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, uint32_t iter
  * to binary16, W dequantized exactly and rounded to binary16, fp32 accumulation. */
 int ribn_rocm_prefill_gemm(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t k, const float *x,
                            uint64_t m, float *y, char *err, size_t err_len);
+/* Q8_1 packing of n values (n a positive multiple of 32) into n/32 * 9 words:
+ * CudaQ8_1Quantizer::execute (nvidia/src/activation.rs; kernel activation.cu:1-28),
+ * bit-identical words. */
+int ribn_rocm_quantize_q8_1(const float *x, uint64_t n, uint32_t *out, char *err, size_t err_len);
+/* Integer-dot matvec of `members` (1..8) Q8_1-packed inputs ([members][k/32 * 9]
+ * words) against a Q8_0 / Q4_K / Q6_K matrix, y [members][rows]:
+ * CudaQ4KQ8_1Gemv / CudaQ6KQ8_1Gemv / CudaQ8_0Q8_1Gemv ::execute and ::execute_batch
+ * (nvidia/src/q4_q8_1.rs, q6_q8_1.rs, q8_0_q8_1.rs). */
+int ribn_rocm_gemv_q8_1(uint32_t type, const uint8_t *blocks, uint64_t rows, uint64_t k, const uint32_t *packed,
+                        uint32_t members, float *y, char *err, size_t err_len);
+/* Time `iters` integer-dot launches on device-resident data (HIP events on the launch stream). */
+int ribn_rocm_bench_gemv_q8_1(uint32_t type, uint64_t rows, uint64_t k, uint32_t members, uint32_t iters,
+                              double *avg_ms, char *err, size_t err_len);
 /* Greedy argmax (model_ops.rs:203-260): first maximum, NaN skipped. */
 int ribn_rocm_argmax(const float *logits, uint64_t n, uint32_t *out, char *err, size_t err_len);
 

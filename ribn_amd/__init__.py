@@ -34,6 +34,7 @@ RIBN_OK, RIBN_PENDING = 0, 1
 LOAD_KV_BF16 = 1
 LOAD_PERSISTENT_STEP = 2
 LOAD_RESIDENT_F16 = 4
+LOAD_INT_DOT = 8
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -145,6 +146,11 @@ _sig("ribn_rocm_gemv", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _f
      _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_bench_gemv", _c.c_int, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_uint32, _c.POINTER(_c.c_double),
      _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_quantize_q8_1", _c.c_int, _f32p, _c.c_uint64, _u32p, _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_gemv_q8_1", _c.c_int, _c.c_uint32, _u8p, _c.c_uint64, _c.c_uint64, _u32p, _c.c_uint32, _f32p,
+     _c.c_char_p, _c.c_size_t)
+_sig("ribn_rocm_bench_gemv_q8_1", _c.c_int, _c.c_uint32, _c.c_uint64, _c.c_uint64, _c.c_uint32, _c.c_uint32,
+     _c.POINTER(_c.c_double), _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_argmax", _c.c_int, _f32p, _c.c_uint64, _u32p, _c.c_char_p, _c.c_size_t)
 _sig("ribn_rocm_bench_model_kernel", _c.c_int, _c.c_void_p, _c.c_uint32, _c.c_uint32, _c.POINTER(_c.c_double),
      _c.POINTER(_c.c_uint64), _c.c_char_p, _c.c_size_t)
@@ -250,6 +256,34 @@ def bench_gemv(type_: int, rows: int, k: int, iters: int = 50) -> float:
     return ms.value
 
 
+def quantize_q8_1(x: np.ndarray) -> np.ndarray:
+    """Q8_1 words (len(x) / 32 blocks of 9) packed on the device (the reference's quantize_q8_1)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size // 32 * 9, dtype=np.uint32)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_quantize_q8_1(_ptr(x, _f32p), x.size, _ptr(out, _u32p), err, _ERR), err)
+    return out
+
+
+def gemv_q8_1(type_: int, blocks: np.ndarray, rows: int, k: int, packed: np.ndarray, members: int = 1) -> np.ndarray:
+    """Integer-dot matvec of `members` Q8_1-packed inputs on the device: y [members][rows]."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    y = np.empty((members, rows), dtype=np.float32)
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_gemv_q8_1(type_, _ptr(blocks, _u8p), rows, k, _ptr(packed, _u32p), members,
+                                    _ptr(y, _f32p), err, _ERR), err)
+    return y
+
+
+def bench_gemv_q8_1(type_: int, rows: int, k: int, members: int = 1, iters: int = 50) -> float:
+    """Average device milliseconds per integer-dot matvec launch (HIP events)."""
+    ms = ctypes.c_double()
+    err = ctypes.create_string_buffer(_ERR)
+    _check(_lib.ribn_rocm_bench_gemv_q8_1(type_, rows, k, members, iters, ctypes.byref(ms), err, _ERR), err)
+    return ms.value
+
+
 def prefill_gemm(type_: int, blocks: np.ndarray, rows: int, k: int, x: np.ndarray) -> np.ndarray:
     """Y = f16(X) dequant(W)^T with the prefill MFMA GEMM; X is [m][k]."""
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
@@ -308,18 +342,23 @@ class QwenRocm:
     """A loaded dense Qwen GGUF on one MI355X (QwenCuda, crates/qwen/src/cuda.rs:30-121)."""
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
-                 kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain", gemm: str = "dequant"):
+                 kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain", gemm: str = "dequant",
+                 gemv: str = "float"):
         """step: "persistent" (one kernel launch per token step when the library has a kernel compiled for
         this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs).
         gemm: "dequant" (chunked prefill and batched decode on the dequantizing MFMA GEMM) or "resident"
-        (binary16 copies of the weights made at load, hipBLASLt GEMMs)."""
+        (binary16 copies of the weights made at load, hipBLASLt GEMMs).
+        gemv: "float" (default) or "int-dot": sampled decode rows run the lossy integer-dot projections over
+        Q8_1-packed inputs (the reference's GemvMode::IntegerDot)."""
+        if gemv not in ("float", "int-dot"):
+            raise ValueError("gemv must be 'float' or 'int-dot'")
         if gemm not in ("dequant", "resident"):
             raise ValueError("gemm must be 'dequant' or 'resident'")
         if step not in ("persistent", "chain"):
             raise ValueError("step must be 'persistent' or 'chain'")
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
                            (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0)
-                           | (LOAD_RESIDENT_F16 if gemm == "resident" else 0))
+                           | (LOAD_RESIDENT_F16 if gemm == "resident" else 0) | (LOAD_INT_DOT if gemv == "int-dot" else 0))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()

@@ -329,4 +329,32 @@ hipError_t launch_step(const StepArgs& a, const StepKey& key, int n_wg, size_t l
 hipError_t launch_argmax(const float* logits, uint32_t n, uint64_t* partial, uint32_t* counter,
                          uint32_t* out, hipStream_t stream);
 
+// ---------------------------------------------------------------------------
+// Integer-dot projections (the reference's GemvMode::IntegerDot): inputs packed
+// as Q8_1 (per 32 values: word half(d) | half(sum) << 16, then 32 signed bytes
+// q = round(x / d), d = max|x| / 127), weights read once for up to
+// kIdMaxMembers packed inputs.
+constexpr int kIdMaxMembers = 8;
+struct IdArgs {
+    const uint32_t* xq;     // [members][k/32 * 9] Q8_1 words
+    int32_t k;
+    int32_t members;        // 1 .. kIdMaxMembers
+    int32_t ld;             // output / residual row stride (floats) between members
+    int32_t mode;           // MV_STORE (+ bias), MV_ADD or MV_SILU
+    int32_t nseg;
+    int32_t items_per_wave;
+    uint32_t type_a, type_b;   // segments 0, 1: type_a; segment 2: type_b
+    MvSeg seg[3];           // out / res / bias of member m at + m * ld
+};
+// Grid size of the launch after laying the segments out over n_cu compute units.
+int intdot_layout(IdArgs& a, int n_cu);
+hipError_t launch_intdot(const IdArgs& a, int n_wg, hipStream_t stream);
+// Q8_1 words of `rows` rows of k values (k % 32 == 0): x row r at x + r * ldx,
+// words of row r at out + r * (k / 32) * 9. With norm_w, each row is first
+// RMS-normalized: x * (1 / sqrt(mean(x^2) + eps)) * w.
+hipError_t launch_q8_1_rows(const float* x, int ldx, int rows, int k, const float* norm_w, float eps, uint32_t* out,
+                            hipStream_t stream);
+// Q8_1 words of n values (n % 32 == 0) as one flat vector.
+hipError_t launch_quantize_q8_1(const float* x, size_t n, uint32_t* out, hipStream_t stream);
+
 }  // namespace ribn

@@ -137,6 +137,11 @@ struct ribn_rocm_model {
     uint32_t* b_counters = nullptr;
     size_t p_part_floats = 0;
     uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
+    // integer-dot decode (RIBN_LOAD_INT_DOT): Q8_1 words of the decode rows' inputs, SwiGLU rows
+    bool int_dot = false;
+    uint32_t* b_xq = nullptr;
+    float* b_act = nullptr;
+    int cur_slot = 0;   // the slot select_slot last pointed the step at
 
     // persistent step (one launch per token); step_wg == 0: launch chain only
     int step_wg = 0;
@@ -798,6 +803,74 @@ hipError_t prefill_chunk(ribn_rocm_model* M, int slot, int pos0, int m, bool fin
     return e;
 }
 
+int device_cus() {
+    int dev = 0, n = 256;
+    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    return n;
+}
+
+// The layers and head of the decode rows in the integer-dot mode (the
+// reference's GemvMode::IntegerDot, nvidia/src/decode.rs:298-312; its batched
+// executor gemv_batch, decode.rs:1591-1633, 2250-2520): each projection's input
+// rows are packed to Q8_1 (with the RMSNorm before it fused into the packing),
+// then the integer-dot matvec reads the weights once for every group of at
+// most kIdMaxMembers rows. Attention, rope, the caches and the argmax are those
+// of the float rows; the embedding rows are in p_h.
+hipError_t intdot_rows(ribn_rocm_model* M, const DecodeRows& dr, int n_splits) {
+    hipStream_t st = M->stream;
+    const int n = dr.rows;
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd, ldq = qd + 2 * kd;
+    const int n_cu = device_cus();
+    auto seg = [](const QMat& w, float* out, const float* bias = nullptr, const float* res = nullptr) {
+        MvSeg sg{};
+        sg.w = w;
+        sg.out = out;
+        sg.bias = bias;
+        sg.res = res;
+        return sg;
+    };
+    auto proj = [&](const float* x, int k, const float* norm_w, int mode, std::initializer_list<MvSeg> segs, int ld) {
+        const size_t words = (size_t)(k / 32) * 9;
+        hipError_t e = launch_q8_1_rows(x, k, n, k, norm_w, M->eps, M->b_xq, st);
+        for (int r0 = 0; e == hipSuccess && r0 < n; r0 += kIdMaxMembers) {
+            IdArgs a{};
+            a.xq = M->b_xq + (size_t)r0 * words;
+            a.k = k;
+            a.members = std::min(kIdMaxMembers, n - r0);
+            a.ld = ld;
+            a.mode = mode;
+            for (MvSeg sg : segs) {
+                sg.out += (size_t)r0 * ld;
+                if (sg.res) sg.res += (size_t)r0 * ld;
+                a.seg[a.nseg++] = sg;
+            }
+            a.type_a = a.seg[0].w.type;
+            a.type_b = a.seg[a.nseg - 1].w.type;
+            e = launch_intdot(a, intdot_layout(a, n_cu), st);
+        }
+        return e;
+    };
+    hipError_t e = hipSuccess;
+    for (int l = 0; l < M->L; l++) {
+        const Layer& y = M->layers[l];
+        if ((e = proj(M->p_h, M->H, y.attn_norm, MV_STORE,
+                      {seg(y.q, M->p_qkv, y.q_bias), seg(y.k, M->p_qkv + qd, y.k_bias),
+                       seg(y.v, M->p_qkv + qd + kd, y.v_bias)},
+                      ldq)) != hipSuccess)
+            return e;
+        AttnArgs at = attn_args(M, l, n_splits);
+        if ((e = launch_attention_rows(at, dr, st)) != hipSuccess) return e;
+        if ((e = proj(M->b_att, qd, nullptr, MV_ADD, {seg(y.o, M->p_h, nullptr, M->p_h)}, M->H)) != hipSuccess) return e;
+        MvSeg gu = seg(y.gate, M->b_act);
+        gu.w2 = y.up;
+        if ((e = proj(M->p_h, M->H, y.ffn_norm, MV_SILU, {gu}, M->F)) != hipSuccess) return e;
+        if ((e = proj(M->b_act, M->F, nullptr, MV_ADD, {seg(y.down, M->p_h, nullptr, M->p_h)}, M->H)) != hipSuccess)
+            return e;
+    }
+    if ((e = proj(M->p_h, M->H, M->out_norm, MV_STORE, {seg(M->out, M->b_logits)}, M->V)) != hipSuccess) return e;
+    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);
+}
+
 // One decode row per sequence, all in one step (batched decode): row r
 // consumes the token at position pos[r] of the sequence in slot[r] and samples
 // the next one. The projections run as the chunked-prefill MFMA GEMMs over the
@@ -837,6 +910,8 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     if ((e = launch_gather_row_tokens(M->d_tokens, M->context + 1, dr, M->d_btokens, st)) != hipSuccess) return e;
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
+    const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
+    if (M->int_dot) return intdot_rows(M, dr, n_splits);
     auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
                     int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr,
                     const uint16_t* w16 = nullptr, const float* bias16 = nullptr) {
@@ -855,7 +930,6 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
         else g.ksplit = 1;
         return run_gemm(M, g, w16, ldy, bias16, st);
     };
-    const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
         // layer l > 0 receives its normed input from the previous down GEMM
@@ -917,6 +991,8 @@ hipError_t prefill_rows(ribn_rocm_model* M, int slot, int pos0, int n, bool fina
 // trace (device, (L+1) x hidden): residual stream after the embedding and
 // after every layer.
 hipError_t run_step(ribn_rocm_model* M, bool head, int ctx, float* trace) {
+    // integer-dot mode: a sampled step of the active sequence is a decode row
+    if (M->int_dot && head && !trace) return decode_rows(M, {M->cur_slot}, {ctx - 1});
     if (M->step_wg > 0) {
         StepArgs a = M->step_args;
         a.head = head ? 1 : 0;
@@ -945,6 +1021,7 @@ hipError_t step_failed(ribn_rocm_model* M, bool* failed) {
 
 // Point the graphs at `slot` and (re)write its device state from the pinned mirror.
 hipError_t select_slot(ribn_rocm_model* M, int slot) {
+    M->cur_slot = slot;
     return hipMemcpyAsync(M->d_ctl, &M->h_ctl[slot], sizeof(StepCtl), hipMemcpyHostToDevice, M->stream);
 }
 
@@ -1111,8 +1188,9 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             return RIBN_ERR_FORMAT;
         }
         M->channels = 2 * M->ssm_hk * M->ssm_d + M->inner;
-        if (opts && (opts->flags & (RIBN_LOAD_RESIDENT_F16 | RIBN_LOAD_PERSISTENT_STEP))) {
-            set_err(err, err_len, "qwen35 hybrids run the default launch chain (no resident or persistent mode)");
+        if (opts && (opts->flags & (RIBN_LOAD_RESIDENT_F16 | RIBN_LOAD_PERSISTENT_STEP | RIBN_LOAD_INT_DOT))) {
+            set_err(err, err_len, "qwen35 hybrids run the default launch chain (no resident, persistent or "
+                                  "integer-dot mode)");
             return RIBN_ERR_INVALID;
         }
     }
@@ -1149,6 +1227,11 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     if ((int)M->kv_pages < M->max_pages) M->kv_pages = M->max_pages;
     M->device = o.device;
     M->kv_f16 = (o.flags & RIBN_LOAD_KV_BF16) == 0;
+    M->int_dot = (o.flags & RIBN_LOAD_INT_DOT) != 0;
+    if (M->int_dot && (o.flags & RIBN_LOAD_PERSISTENT_STEP)) {
+        set_err(err, err_len, "the integer-dot mode runs decode rows, not the persistent step");
+        return RIBN_ERR_INVALID;
+    }
     M->name = "ribn-rocm " + arch + " " + std::to_string(M->L) + "x" + std::to_string(M->H);
 
     HIPCHK(hipSetDevice(M->device));
@@ -1374,7 +1457,9 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
         // batched decode rows: one per sequence, at most the chunk's rows
         // (hybrids decode one sequence per step: the recurrent blocks have no batched form here)
         M->b_rows = M->hybrid ? 0 : (int)std::min<size_t>(c, M->max_seqs);
-        if (M->b_rows >= 2) {
+        // the integer-dot mode runs every sampled decode row here, also one at a time
+        if (M->int_dot) M->b_rows = std::max(M->b_rows, 1);
+        if (M->b_rows >= 2 || M->int_dot) {
             const size_t R = (size_t)M->b_rows;
             M->b_part_stride = (size_t)M->hkv * kMaxSplits * ((size_t)(M->hq / M->hkv) * M->hd + 2 * (M->hq / M->hkv));
             HIPCHK(dalloc(M, &M->d_brows, sizeof(int32_t) * 2 * R));
@@ -1386,6 +1471,10 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             HIPCHK(dalloc(M, &M->b_counters, sizeof(uint32_t) * R * M->hkv));
             HIPCHK(hipMemsetAsync(M->b_counters, 0, sizeof(uint32_t) * R * M->hkv, M->stream));
             M->h_brows.assign(2 * R, 0);
+            if (M->int_dot) {
+                HIPCHK(dalloc(M, &M->b_xq, sizeof(uint32_t) * R * (kmax / 32) * 9));
+                HIPCHK(dalloc(M, &M->b_act, sizeof(float) * R * M->F));
+            }
         }
     }
 
@@ -1416,6 +1505,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     }
     HIPCHK(hipMemcpyAsync(M->d_slots, M->h_state, sizeof(SeqState) * slots, hipMemcpyHostToDevice, M->stream));
     HIPCHK(hipMemcpyAsync(M->d_ctl, &M->h_ctl[slots - 1], sizeof(StepCtl), hipMemcpyHostToDevice, M->stream));
+    M->cur_slot = slots - 1;
     HIPCHK(hipStreamSynchronize(M->stream));
     for (int s = (int)M->max_seqs - 1; s >= 0; s--) M->free_slots.push_back(s);
     for (int p = (int)M->kv_pages - 1; p >= 0; p--) M->free_pages.push_back(p);
@@ -1513,6 +1603,8 @@ extern "C" int ribn_rocm_trace(ribn_rocm_model* M, const uint32_t* tokens, uint3
     if (!M || !tokens || !argmax_out) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
     if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
     if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    if (M->int_dot)
+        return fail(nullptr, err, err_len, "traces run the float projections: not in the integer-dot mode", RIBN_ERR_INVALID);
     if (n == 0 || n + 1 > M->context) return fail(nullptr, err, err_len, "trace length outside the context", RIBN_ERR_INVALID);
     for (uint32_t i = 0; i < n; i++)
         if (tokens[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
@@ -1675,18 +1767,22 @@ extern "C" int ribn_rocm_submit(ribn_rocm_model* M, const ribn_rocm_batch_item* 
     // decode rows (one token, sampled) of two or more sequences run as one batched step
     std::vector<char> batched(n, 0);
     M->last_batch_seqs.clear();
-    if (M->b_rows >= 2 && M->step_wg == 0) {
+    // (in the integer-dot mode every sampled decode row, also a single one)
+    const size_t min_rows = M->int_dot ? 1 : 2;
+    if (M->b_rows >= (int)min_rows && M->step_wg == 0) {
         std::vector<int> bslots, bpos;
         std::vector<size_t> brow;
         for (size_t r = 0; r < n; r++) {
             const ribn_rocm_batch_item& it = items[r];
-            if (it.kind == RIBN_STEP_DECODE && it.token_budget == 1 && it.output_budget == 1 && (int)bslots.size() < M->b_rows) {
+            // a one-token prompt row that samples is a decode row too (integer-dot mode)
+            const bool row = it.kind == RIBN_STEP_DECODE || M->int_dot;
+            if (row && it.token_budget == 1 && it.output_budget == 1 && (int)bslots.size() < M->b_rows) {
                 bslots.push_back(M->seqs[it.sequence].slot);
                 bpos.push_back((int)it.prefix);
                 brow.push_back(r);
             }
         }
-        if (bslots.size() >= 2) {
+        if (bslots.size() >= min_rows) {
             for (size_t i = 0; i < brow.size(); i++) {
                 batched[brow[i]] = 1;
                 M->seqs[items[brow[i]].sequence].in_flight = true;
@@ -1939,6 +2035,110 @@ extern "C" int ribn_rocm_bench_gemv(uint32_t type, uint64_t rows, uint64_t k, ui
     return RIBN_OK;
 }
 
+extern "C" int ribn_rocm_quantize_q8_1(const float* x, uint64_t n, uint32_t* out, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    if (!x || !out) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
+    if (n == 0 || n % 32)
+        return fail(nullptr, err, err_len, "Q8_1 input length must be a positive multiple of 32", RIBN_ERR_INVALID);
+    Scoped S;
+    float* dx = nullptr;
+    uint32_t* dq = nullptr;
+    HIPCHK(S.alloc(&dx, sizeof(float) * n));
+    HIPCHK(S.alloc(&dq, sizeof(uint32_t) * (n / 32) * 9));
+    HIPCHK(hipMemcpy(dx, x, sizeof(float) * n, hipMemcpyHostToDevice));
+    HIPCHK(launch_quantize_q8_1(dx, n, dq, nullptr));
+    HIPCHK(hipMemcpy(out, dq, sizeof(uint32_t) * (n / 32) * 9, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
+
+std::string check_intdot(uint32_t type, uint64_t rows, uint64_t k, uint32_t members) {
+    std::string m = check_shape(type, rows, k);
+    if (!m.empty()) return m;
+    if (type != 8 && type != 12 && type != 14) return "no integer-dot kernel for this value type";
+    if (members < 1 || members > (uint32_t)kIdMaxMembers) return "members must be 1 .. 8";
+    if (rows > 0x7fffffffu / members) return "output too large";
+    return "";
+}
+
+extern "C" int ribn_rocm_gemv_q8_1(uint32_t type, const uint8_t* blocks, uint64_t rows, uint64_t k,
+                                   const uint32_t* packed, uint32_t members, float* y, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string m = check_intdot(type, rows, k, members);
+    if (!m.empty() || !blocks || !packed || !y)
+        return fail(nullptr, err, err_len, m.empty() ? "null argument" : m, RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    uint32_t* dq = nullptr;
+    float* dy = nullptr;
+    const size_t words = (size_t)members * (k / 32) * 9;
+    HIPCHK(upload_plain(S, type, rows, k, blocks, &q));
+    HIPCHK(S.alloc(&dq, sizeof(uint32_t) * words));
+    HIPCHK(S.alloc(&dy, sizeof(float) * rows * members));
+    HIPCHK(hipMemcpy(dq, packed, sizeof(uint32_t) * words, hipMemcpyHostToDevice));
+    IdArgs a{};
+    a.xq = dq;
+    a.k = (int)k;
+    a.members = (int)members;
+    a.ld = (int)rows;
+    a.mode = MV_STORE;
+    a.nseg = 1;
+    a.type_a = a.type_b = type;
+    a.seg[0].w = q;
+    a.seg[0].out = dy;
+    const int nwg = intdot_layout(a, device_cus());
+    HIPCHK(launch_intdot(a, nwg, nullptr));
+    HIPCHK(hipMemcpy(y, dy, sizeof(float) * rows * members, hipMemcpyDeviceToHost));
+    return RIBN_OK;
+}
+
+extern "C" int ribn_rocm_bench_gemv_q8_1(uint32_t type, uint64_t rows, uint64_t k, uint32_t members, uint32_t iters,
+                                         double* avg_ms, char* err, size_t err_len) {
+    ribn_rocm_model* M = nullptr;
+    std::string m = check_intdot(type, rows, k, members);
+    if (!m.empty() || !avg_ms || iters == 0)
+        return fail(nullptr, err, err_len, m.empty() ? "bad argument" : m, RIBN_ERR_INVALID);
+    Scoped S;
+    QMat q;
+    float *dx = nullptr, *dy = nullptr;
+    uint32_t* dq = nullptr;
+    HIPCHK(upload_plain(S, type, rows, k, nullptr, &q));
+    HIPCHK(S.alloc(&dx, sizeof(float) * k * members));
+    HIPCHK(S.alloc(&dq, sizeof(uint32_t) * members * (k / 32) * 9));
+    HIPCHK(S.alloc(&dy, sizeof(float) * rows * members));
+    std::vector<float> hx(k * members);
+    for (size_t i = 0; i < hx.size(); i++) hx[i] = (float)((int)(i * 37 % 101) - 50) * 0.01f;
+    HIPCHK(hipMemcpy(dx, hx.data(), sizeof(float) * hx.size(), hipMemcpyHostToDevice));
+    HIPCHK(launch_quantize_q8_1(dx, hx.size(), dq, nullptr));
+    IdArgs a{};
+    a.xq = dq;
+    a.k = (int)k;
+    a.members = (int)members;
+    a.ld = (int)rows;
+    a.mode = MV_STORE;
+    a.nseg = 1;
+    a.type_a = a.type_b = type;
+    a.seg[0].w = q;
+    a.seg[0].out = dy;
+    const int nwg = intdot_layout(a, device_cus());
+    hipStream_t st;
+    HIPCHK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    for (int i = 0; i < 3; i++) HIPCHK(launch_intdot(a, nwg, st));
+    HIPCHK(hipEventRecord(e0, st));
+    for (uint32_t i = 0; i < iters; i++) HIPCHK(launch_intdot(a, nwg, st));
+    HIPCHK(hipEventRecord(e1, st));
+    HIPCHK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+    *avg_ms = ms / iters;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipStreamDestroy(st);
+    return RIBN_OK;
+}
+
 extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, uint32_t iters, double* avg_ms,
                                             uint64_t* bytes, char* err, size_t err_len) {
     if (!M || !avg_ms || !bytes || iters == 0) return fail(nullptr, err, err_len, "bad argument", RIBN_ERR_INVALID);
@@ -2096,6 +2296,8 @@ extern "C" int ribn_rocm_prefill_trace(ribn_rocm_model* M, const uint32_t* token
     if (!M || !tokens) return fail(nullptr, err, err_len, "null argument", RIBN_ERR_INVALID);
     if (M->faulted) return fail(nullptr, err, err_len, "ROCm execution is faulted", RIBN_ERR_FAULTED);
     if (M->has_pending) return fail(nullptr, err, err_len, "a submission is in flight", RIBN_ERR_BUSY);
+    if (M->int_dot)
+        return fail(nullptr, err, err_len, "traces run the float projections: not in the integer-dot mode", RIBN_ERR_INVALID);
     if (n == 0 || n + 1 > M->context) return fail(nullptr, err, err_len, "trace length outside the context", RIBN_ERR_INVALID);
     for (uint32_t i = 0; i < n; i++)
         if (tokens[i] >= (uint32_t)M->V) return fail(nullptr, err, err_len, "token id out of range", RIBN_ERR_INVALID);
