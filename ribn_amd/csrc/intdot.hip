@@ -61,34 +61,38 @@ __device__ __forceinline__ void pack_block(float v, uint32_t* blk, bool valid) {
                  ((uint32_t)__half_as_ushort(__float2half_rn(s)) << 16);
 }
 
-// One workgroup per row: optional RMSNorm (rms_norm, model_ops.rs:108: x *
-// inv * w with inv = 1 / sqrt(sum / n + eps)), then the row's blocks, one per
-// half-wave at a time.
+// Workgroup (x, r): blocks 8x .. 8x + 7 of row r, one per half-wave. With a
+// norm (rms_norm, model_ops.rs:108: x * inv * w with inv = 1 / sqrt(sum / n +
+// eps)) every workgroup of the row sums the row's squares itself (the row is
+// a few KB in L2), so the packing needs no second launch.
 __global__ __launch_bounds__(256) void q8_1_rows_kernel(const float* x, int ldx, int k, const float* norm_w, float eps,
                                                         uint32_t* out) {
     __shared__ float red[4];
-    const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* xr = x + (size_t)r * ldx;
-    uint32_t* o = out + (size_t)r * (k / 32) * 9;
+    const int nb = k / 32;
+    const int b = blockIdx.x * 8 + (tid >> 5);
+    const bool valid = b < nb;
+    const int i = valid ? b * 32 + (tid & 31) : 0;
+    float v = xr[i];
     float inv = 1.0f;
     if (norm_w) {
-        float ss = 0.f;
-        for (int i = tid; i < k; i += 256) ss += xr[i] * xr[i];
-        ss = wave_sum(ss);
+        const float w = norm_w[i];
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+        int j = tid;
+        for (; j + 768 < k; j += 1024) {
+            const float a0 = xr[j], a1 = xr[j + 256], a2 = xr[j + 512], a3 = xr[j + 768];
+            s0 += a0 * a0; s1 += a1 * a1; s2 += a2 * a2; s3 += a3 * a3;
+        }
+        for (; j < k; j += 256) s0 += xr[j] * xr[j];
+        float ss = wave_sum((s0 + s1) + (s2 + s3));
         if (lane == 0) red[wave] = ss;
         __syncthreads();
         ss = red[0] + red[1] + red[2] + red[3];
         inv = 1.0f / sqrtf(ss / (float)k + eps);
+        v = v * inv * w;
     }
-    const int nb = k / 32;
-    for (int b0 = 0; b0 < nb; b0 += 8) {
-        const int b = b0 + (tid >> 5);
-        const bool valid = b < nb;
-        const int i = valid ? b * 32 + (tid & 31) : 0;
-        float v = xr[i];
-        if (norm_w) v = v * inv * norm_w[i];
-        pack_block(v, o + (size_t)(valid ? b : 0) * 9, valid);
-    }
+    pack_block(v, out + ((size_t)r * nb + (valid ? b : 0)) * 9, valid);
 }
 
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* x, size_t nb, uint32_t* out) {
@@ -504,7 +508,7 @@ hipError_t launch_intdot(const IdArgs& a, int n_wg, hipStream_t st) {
 hipError_t launch_q8_1_rows(const float* x, int ldx, int rows, int k, const float* norm_w, float eps, uint32_t* out,
                             hipStream_t st) {
     if (rows <= 0 || k <= 0 || k % 32) return hipErrorInvalidValue;
-    q8_1_rows_kernel<<<rows, 256, 0, st>>>(x, ldx, k, norm_w, eps, out);
+    q8_1_rows_kernel<<<dim3((unsigned)(k / 32 + 7) / 8, (unsigned)rows), 256, 0, st>>>(x, ldx, k, norm_w, eps, out);
     return hipGetLastError();
 }
 

@@ -302,8 +302,9 @@ hipError_t launch_gather_row_tokens(const uint32_t* tokens, int ld, const Decode
                                     hipStream_t stream);
 // greedy argmax of each row of logits [rows][V] (first maximum, NaN skipped), written as the
 // next token of the row's sequence: tokens[pos + 1], last_token, and pos advanced by one
+// (part: [rows][64] scratch keys)
 hipError_t launch_rows_argmax_commit(const float* logits, int V, const DecodeRows& r, SeqState* slots,
-                                     hipStream_t stream);
+                                     uint64_t* part, hipStream_t stream);
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream);
 hipError_t launch_advance(const StepCtl* ctl, hipStream_t stream);
 hipError_t launch_dequant(const QMat& w, float* out, hipStream_t stream);

@@ -161,20 +161,35 @@ __global__ void gather_row_tokens_kernel(const uint32_t* tokens, int ld, DecodeR
     if (row < r.rows) out[row] = tokens[(size_t)r.slot[row] * ld + r.pos[row]];
 }
 
-__global__ __launch_bounds__(1024) void rows_argmax_commit_kernel(const float* logits, int V, DecodeRows r,
-                                                                  SeqState* slots) {
-    __shared__ uint64_t wbest[16];
-    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Greedy argmax of each row of logits in two launches: workgroup (c, row) keeps
+// the best key of chunk c of the row (kArgChunks chunks, all loads of a thread
+// issued together), then one wave per row reduces the chunk keys and commits the
+// token (first maximum, NaN skipped: the packed key orders by value, then by
+// lowest index).
+constexpr int kArgChunks = 64;
+__global__ __launch_bounds__(256) void rows_argmax_part_kernel(const float* logits, int V, uint64_t* part) {
+    __shared__ uint64_t wbest[4];
+    const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* lg = logits + (size_t)row * V;
+    const int per = (V + kArgChunks - 1) / kArgChunks;
+    const int lo = c * per, hi = min(V, lo + per);
     uint64_t b = 0ull;
-    for (int i = tid; i < V; i += 1024) b = max(b, argmax_key(lg[i], (uint32_t)i));
+#pragma unroll 4
+    for (int i = lo + tid; i < hi; i += 256) b = max(b, argmax_key(lg[i], (uint32_t)i));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
     if (lane == 0) wbest[wave] = b;
     __syncthreads();
-    if (tid == 0) {
-        for (int i = 1; i < 16; i++) wbest[0] = max(wbest[0], wbest[i]);
-        const uint32_t tok = wbest[0] ? 0xffffffffu - (uint32_t)(wbest[0] & 0xffffffffu) : 0u;
+    if (tid == 0) part[(size_t)row * kArgChunks + c] = max(max(wbest[0], wbest[1]), max(wbest[2], wbest[3]));
+}
+
+__global__ __launch_bounds__(64) void rows_argmax_commit_kernel(const uint64_t* part, DecodeRows r, SeqState* slots) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    uint64_t b = part[(size_t)row * kArgChunks + lane];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) b = max(b, (uint64_t)__shfl_xor(b, o));
+    if (lane == 0) {
+        const uint32_t tok = b ? 0xffffffffu - (uint32_t)(b & 0xffffffffu) : 0u;
         SeqState* s = &slots[r.slot[row]];
         const int pos = r.pos[row];
         if (pos + 1 <= s->max_ctx) s->tokens[pos + 1] = tok;
@@ -311,8 +326,12 @@ hipError_t launch_gather_row_tokens(const uint32_t* tokens, int ld, const Decode
 }
 
 hipError_t launch_rows_argmax_commit(const float* logits, int V, const DecodeRows& r, SeqState* slots,
-                                     hipStream_t st) {
-    rows_argmax_commit_kernel<<<r.rows, 1024, 0, st>>>(logits, V, r, slots);
+                                     uint64_t* part, hipStream_t st) {
+    static_assert(kArgChunks == 64, "one lane per chunk in the commit kernel");
+    rows_argmax_part_kernel<<<dim3(kArgChunks, r.rows), 256, 0, st>>>(logits, V, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    rows_argmax_commit_kernel<<<r.rows, 64, 0, st>>>(part, r, slots);
     return hipGetLastError();
 }
 

@@ -122,6 +122,7 @@ struct ribn_rocm_model {
     std::vector<int> wg_qkv, wg_o, wg_gu, wg_down;
     MvArgs mv_head{};
     std::map<int, hipGraphExec_t> graphs;   // key: n_splits * 2 + head
+    std::map<int, hipGraphExec_t> row_graphs;   // decode rows, key: rows * 64 + n_splits
 
     // chunked prefill buffers (prefill.hip), rows per chunk = chunk
     int chunk = 0;
@@ -135,6 +136,7 @@ struct ribn_rocm_model {
     std::vector<uint64_t> last_batch_seqs;   // sequences of the last submission's batched decode rows
     size_t b_part_stride = 0;
     uint32_t* b_counters = nullptr;
+    uint64_t* b_argmax = nullptr;          // [b_rows][64] per-chunk argmax keys
     size_t p_part_floats = 0;
     uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
     // integer-dot decode (RIBN_LOAD_INT_DOT): Q8_1 words of the decode rows' inputs, SwiGLU rows
@@ -868,26 +870,20 @@ hipError_t intdot_rows(ribn_rocm_model* M, const DecodeRows& dr, int n_splits) {
             return e;
     }
     if ((e = proj(M->p_h, M->H, M->out_norm, MV_STORE, {seg(M->out, M->b_logits)}, M->V)) != hipSuccess) return e;
-    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);
+    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, M->b_argmax, st);
 }
 
-// One decode row per sequence, all in one step (batched decode): row r
-// consumes the token at position pos[r] of the sequence in slot[r] and samples
-// the next one. The projections run as the chunked-prefill MFMA GEMMs over the
-// rows; attention is the split-K decode kernel over each row's own cache; the
-// head is one GEMM over the rows followed by a per-row argmax.
-hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const std::vector<int>& pos) {
+// The projections of batched decode rows run as the chunked-prefill MFMA GEMMs
+// over the rows (or the integer-dot matvec); attention is the split-K decode
+// kernel over each row's own cache; the head is one GEMM over the rows followed
+// by a per-row argmax.
+// The launches of a decode-rows step for n rows and a split dimension of
+// n_splits: they read the rows' slots and positions from d_brows only, so one
+// captured graph serves every step with the same (n, n_splits).
+hipError_t decode_rows_body(ribn_rocm_model* M, int n, int n_splits) {
     hipStream_t st = M->stream;
-    const int n = (int)slots.size();
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd, ldq = qd + 2 * kd;
-    int max_ctx = 0;
-    for (int r = 0; r < n; r++) {
-        M->h_brows[r] = slots[r];
-        M->h_brows[n + r] = pos[r];
-        max_ctx = std::max(max_ctx, pos[r] + 1);
-    }
-    hipError_t e = hipMemcpyAsync(M->d_brows, M->h_brows.data(), sizeof(int32_t) * 2 * n, hipMemcpyHostToDevice, st);
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
     DecodeRows dr{};
     dr.rows = n;
     dr.slot = M->d_brows;
@@ -910,7 +906,6 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     if ((e = launch_gather_row_tokens(M->d_tokens, M->context + 1, dr, M->d_btokens, st)) != hipSuccess) return e;
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
-    const int n_splits = rows_splits(max_ctx, dr.split_tokens);   // the grid's split dimension
     if (M->int_dot) return intdot_rows(M, dr, n_splits);
     auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
                     int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr,
@@ -960,7 +955,45 @@ hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const 
     if ((e = gemm(M->p_x16, M->H, M->b_logits, M->V, MV_STORE, {PrefillSeg{M->out, 0, 0, nullptr}}, GEMM_POST_NONE,
                   nullptr, nullptr, M->w16_head)) != hipSuccess)
         return e;
-    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, st);
+    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, M->b_argmax, st);
+}
+
+// One decode row per sequence, all in one step (batched decode): row r
+// consumes the token at position pos[r] of the sequence in slot[r] and samples
+// the next one. The rows go to d_brows, then the step's launches replay from a
+// HIP graph keyed by (rows, splits) (captured on first use; eager with
+// RIBN_ROCM_EAGER=1 or resident binary16 weights, whose library GEMMs stay out
+// of graphs).
+hipError_t decode_rows(ribn_rocm_model* M, const std::vector<int>& slots, const std::vector<int>& pos) {
+    hipStream_t st = M->stream;
+    const int n = (int)slots.size();
+    int max_ctx = 0;
+    for (int r = 0; r < n; r++) {
+        M->h_brows[r] = slots[r];
+        M->h_brows[n + r] = pos[r];
+        max_ctx = std::max(max_ctx, pos[r] + 1);
+    }
+    hipError_t e = hipMemcpyAsync(M->d_brows, M->h_brows.data(), sizeof(int32_t) * 2 * n, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return e;
+    const int n_splits = rows_splits(max_ctx, kMaxSplitTokens);   // the grid's split dimension
+    if (eager_mode() || M->blas) return decode_rows_body(M, n, n_splits);
+    const int key = n * 64 + n_splits;
+    auto it = M->row_graphs.find(key);
+    if (it == M->row_graphs.end()) {
+        hipGraph_t g = nullptr;
+        e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return e;
+        hipError_t e2 = decode_rows_body(M, n, n_splits);
+        e = hipStreamEndCapture(st, &g);
+        if (e2 != hipSuccess) { if (g) hipGraphDestroy(g); return e2; }
+        if (e != hipSuccess) return e;
+        hipGraphExec_t ex = nullptr;
+        e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e != hipSuccess) return e;
+        it = M->row_graphs.emplace(key, ex).first;
+    }
+    return hipGraphLaunch(it->second, st);
 }
 
 // Prompt rows pos0 .. pos0 + n - 1 of the sequence in `slot` in chunks of at
@@ -1468,6 +1501,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             HIPCHK(dalloc(M, &M->b_rope, sizeof(float) * R * M->rot));
             HIPCHK(dalloc(M, &M->b_part, sizeof(float) * R * M->b_part_stride));
             HIPCHK(dalloc(M, &M->b_logits, sizeof(float) * R * M->V));
+            HIPCHK(dalloc(M, &M->b_argmax, sizeof(uint64_t) * R * 64));
             HIPCHK(dalloc(M, &M->b_counters, sizeof(uint32_t) * R * M->hkv));
             HIPCHK(hipMemsetAsync(M->b_counters, 0, sizeof(uint32_t) * R * M->hkv, M->stream));
             M->h_brows.assign(2 * R, 0);
@@ -1520,6 +1554,7 @@ extern "C" void ribn_rocm_free(ribn_rocm_model* M) {
     if (!M) return;
     if (M->stream) hipStreamSynchronize(M->stream);
     for (auto& kv : M->graphs) hipGraphExecDestroy(kv.second);
+    for (auto& kv : M->row_graphs) hipGraphExecDestroy(kv.second);
     if (M->pending.done) hipEventDestroy(M->pending.done);
     blas_destroy(M->blas);
     for (void* p : M->dev_allocs) hipFree(p);
