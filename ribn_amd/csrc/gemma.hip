@@ -79,22 +79,120 @@ __global__ __launch_bounds__(256) void project_kernel(const uint16_t* x, int ldx
     y[(size_t)r * ldy + n] = to_bf(sum);
 }
 
-// rms_norm / rms_norm_scale_free (cpu/norm.rs:41-82): one workgroup per row;
-// the energy is summed in order by one thread.
-__global__ __launch_bounds__(256) void rms_kernel(const uint16_t* x, int ldx, int width, float eps,
-                                                  const uint16_t* scale, uint16_t* y, int ldy) {
-    __shared__ float inv;
-    const uint16_t* row = x + (size_t)blockIdx.x * ldx;
-    if (threadIdx.x == 0) {
-        float e = 0.f;
-        for (int i = 0; i < width; i++) {
-            const float v = ld_bf(row[i]);
-            e = __fadd_rn(e, __fmul_rn(v, v));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+// The same projection for one to four rows, built for latency: workgroup b
+// owns output columns [b C, b C + C) of every row. Its 256 threads first copy
+// the K x C weight slab and the input rows into LDS as FP32 (exact: BF16 is a
+// truncated FP32), every global load in flight at once. The slab is stored
+// transposed, K + 1 words per column, so lane c's reads fall on distinct banks.
+// Thread (row, c) then forms bf16(sum_k x[row][k] w[k][c]), k ascending with
+// separately rounded multiplies and adds: the same sum as project_kernel, bit
+// for bit, at two VALU instructions per k. C is a power of two in [8, 64] with
+// K C <= 32768 (128 KB of slab); N and K are multiples of 8.
+__global__ __launch_bounds__(256) void project_cols_kernel(const uint16_t* x, int ldx, int rows, const uint16_t* wt,
+                                                           int K, int N, int C, uint16_t* y, int ldy) {
+    extern __shared__ __attribute__((aligned(16))) float ldsf[];
+    const int KW = K + 1;                                          // words per column
+    float* ws = ldsf;                                              // [C][KW]
+    float* xs = ldsf + ((size_t)C * KW + 3) / 4 * 4;               // [rows][K], 16-byte aligned
+    const int n0 = blockIdx.x * C, tid = threadIdx.x;
+    const int cols = min(C, N - n0);
+    const int cpr = C / 8;                    // 16-byte chunks per slab row of the global layout
+    const int total = (K / 2) * cpr;          // <= 2048 (K C <= 32768): at most 8 per thread
+    u4v v0[8], v1[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int j = q * 256 + tid;
+        const int kp = j / cpr, cc = (j % cpr) * 8;
+        v0[q] = v1[q] = u4v{0u, 0u, 0u, 0u};
+        if (j < total && cc < cols) {
+            v0[q] = *reinterpret_cast<const u4v*>(wt + (size_t)(2 * kp) * N + n0 + cc);
+            v1[q] = *reinterpret_cast<const u4v*>(wt + (size_t)(2 * kp + 1) * N + n0 + cc);
         }
-        const float mean = __fdiv_rn(e, (float)width);
-        inv = (float)pow((double)__fadd_rn(mean, eps), -0.5);
+    }
+    // the input rows: 16-byte chunks of 8 values, at most 8 per thread
+    const int xch = rows * (K / 8);
+    u4v xv[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int j = q * 256 + tid;
+        xv[q] = j < xch ? *reinterpret_cast<const u4v*>(x + (size_t)(j / (K / 8)) * ldx + (j % (K / 8)) * 8)
+                        : u4v{0u, 0u, 0u, 0u};
+    }
+    auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
+    auto hi = [](uint32_t w) { return __uint_as_float(w & 0xffff0000u); };
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int j = q * 256 + tid;
+        if (j >= total) break;
+        const int kp = j / cpr, cc = (j % cpr) * 8;
+        const uint32_t a[4] = {v0[q].x, v0[q].y, v0[q].z, v0[q].w}, b[4] = {v1[q].x, v1[q].y, v1[q].z, v1[q].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float* col = ws + (size_t)(cc + i) * KW + 2 * kp;
+            col[0] = (i & 1) ? hi(a[i >> 1]) : lo(a[i >> 1]);
+            col[1] = (i & 1) ? hi(b[i >> 1]) : lo(b[i >> 1]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int j = q * 256 + tid;
+        if (j < xch) {
+            const uint32_t a[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+            float4* dst = reinterpret_cast<float4*>(xs + (size_t)j * 8);
+            dst[0] = float4{lo(a[0]), hi(a[0]), lo(a[1]), hi(a[1])};
+            dst[1] = float4{lo(a[2]), hi(a[2]), lo(a[3]), hi(a[3])};
+        }
     }
     __syncthreads();
+    const int r = tid / C, c = tid % C;
+    if (r >= rows || c >= cols) return;
+    const float4* xr = reinterpret_cast<const float4*>(xs + (size_t)r * K);
+    const float* wr = ws + (size_t)c * KW;
+    float sum = 0.f;
+    for (int k4 = 0; k4 < K / 4; k4++) {
+        const float4 xq = xr[k4];
+        const float w0 = wr[4 * k4], w1 = wr[4 * k4 + 1], w2 = wr[4 * k4 + 2], w3 = wr[4 * k4 + 3];
+        sum = __fadd_rn(sum, __fmul_rn(xq.x, w0));
+        sum = __fadd_rn(sum, __fmul_rn(xq.y, w1));
+        sum = __fadd_rn(sum, __fmul_rn(xq.z, w2));
+        sum = __fadd_rn(sum, __fmul_rn(xq.w, w3));
+    }
+    y[(size_t)r * ldy + n0 + c] = to_bf(sum);
+}
+
+// rms_norm / rms_norm_scale_free (cpu/norm.rs:41-82): one workgroup per row.
+// The squares are formed by all threads into LDS (each rounded as the
+// reference rounds it); one thread then adds them in index order, reading LDS
+// eight at a time, so the energy is the reference's sequential sum.
+__global__ __launch_bounds__(256) void rms_kernel(const uint16_t* x, int ldx, int width, float eps,
+                                                  const uint16_t* scale, uint16_t* y, int ldy, const int* dpos,
+                                                  size_t ypos) {
+    extern __shared__ float sq[];
+    if (dpos) y += (size_t)*dpos * ypos;   // graph replays: the output row follows the device position   // [width] squares, then the inverse at [width]
+    const uint16_t* row = x + (size_t)blockIdx.x * ldx;
+    for (int i = threadIdx.x; i < width; i += 256) {
+        const float v = ld_bf(row[i]);
+        sq[i] = __fmul_rn(v, v);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float e = 0.f;
+        int i = 0;
+        for (; i + 8 <= width; i += 8) {
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) t[j] = sq[i + j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) e = __fadd_rn(e, t[j]);
+        }
+        for (; i < width; i++) e = __fadd_rn(e, sq[i]);
+        const float mean = __fdiv_rn(e, (float)width);
+        sq[width] = (float)pow((double)__fadd_rn(mean, eps), -0.5);
+    }
+    __syncthreads();
+    const float inv = sq[width];
     for (int i = threadIdx.x; i < width; i += 256) {
         float v = __fmul_rn(ld_bf(row[i]), inv);
         if (scale) v = __fmul_rn(v, ld_bf(scale[i]));
@@ -147,7 +245,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, int w
 
 // split-half rotary with BF16-rounded products (cpu/rotary.rs:88-134)
 __global__ __launch_bounds__(256) void rotary_kernel(const uint16_t* x, int rows, int heads, int width,
-                                                     const uint16_t* cs, const uint16_t* sn, uint16_t* y) {
+                                                     const uint16_t* cs, const uint16_t* sn, uint16_t* y,
+                                                     const int* dpos, size_t ypos) {
+    if (dpos) y += (size_t)*dpos * ypos;
     const int half = width / 2;
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (size_t)rows * heads * half) return;
@@ -169,8 +269,13 @@ __global__ __launch_bounds__(256) void rotary_kernel(const uint16_t* x, int rows
 // softmax total summed in key order by one thread; output columns summed in key order.
 __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* q, int seq, const uint16_t* keys,
                                                         const uint16_t* values, int kv_seq, int heads, int kv_heads,
-                                                        int width, int window, int q_start, uint16_t* out) {
+                                                        int width, int window, int q_start, uint16_t* out,
+                                                        const int* dpos) {
     extern __shared__ float sc[];   // [kv_seq] scores, then weights
+    if (dpos) {   // graph replays: the chunk starts at the device position
+        q_start = *dpos;
+        kv_seq = q_start + seq;
+    }
     __shared__ float stat[2];
     const int pos = blockIdx.x, h = blockIdx.y;
     const int kvh = h / (heads / kv_heads);
@@ -187,6 +292,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* q, int s
     for (int t = first + threadIdx.x; t <= last; t += 256) {
         const uint16_t* kr = keys + (size_t)t * kv_step + (size_t)kvh * width;
         float s = 0.f;
+#pragma unroll 8
         for (int i = 0; i < width; i++) s = __fadd_rn(s, __fmul_rn(ld_bf(qr[i]), ld_bf(kr[i])));
         sc[t] = ld_bf(to_bf(s));
     }
@@ -209,6 +315,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* q, int s
     __syncthreads();
     for (int i = threadIdx.x; i < width; i += 256) {
         float acc = 0.f;
+#pragma unroll 8
         for (int t = first; t <= last; t++)
             acc = __fadd_rn(acc, __fmul_rn(sc[t], ld_bf(values[(size_t)t * kv_step + (size_t)kvh * width + i])));
         out[(size_t)pos * head_step + (size_t)h * width + i] = to_bf(acc);
@@ -268,6 +375,13 @@ struct ribn_rocm_gemma {
     float embed_scale = 0.f, ple_embed_scale = 0.f, ple_projection_scale = 0.f;
     bool faulted = false;
     std::vector<float> inv_freq[ribn::kMaxLayers];
+    // graph-replayed decode rows: device position and rotary factors of the row,
+    // their pinned host sources, and the captured step
+    int* d_pos = nullptr;
+    uint16_t* d_rot = nullptr;       // [2][layers][maxhd]: cos, then sin
+    uint32_t* h_step = nullptr;      // pinned: token, position
+    uint16_t* h_rot = nullptr;       // pinned: as d_rot
+    hipGraphExec_t decode_graph = nullptr;
 };
 
 namespace ribn {
@@ -456,6 +570,9 @@ extern "C" void ribn_rocm_gemma_close(ribn_rocm_gemma* G) {
     if (!G) return;
     hipSetDevice(G->device);
     if (G->stream) hipStreamSynchronize(G->stream);
+    if (G->decode_graph) hipGraphExecDestroy(G->decode_graph);
+    if (G->h_step) hipHostFree(G->h_step);
+    if (G->h_rot) hipHostFree(G->h_rot);
     for (void* p : G->allocs) hipFree(p);
     if (G->stream) hipStreamDestroy(G->stream);
     delete G;
@@ -637,6 +754,13 @@ extern "C" int ribn_rocm_gemma_open(const char* package_dir, int32_t device, rib
          galloc(G, &G->logits, 2 * (size_t)c.vocab) == hipSuccess && galloc(G, &G->tokens, 4 * R) == hipSuccess;
     if (!ok) return bail(gfail(err, err_len, "device allocation failed", RIBN_ERR_DEVICE));
     G->maxhd = maxhd;
+    // decode rows replay a graph when every score of a row fits the attention kernel's LDS
+    if (4 * (size_t)c.context <= 60 * 1024) {
+        ok = galloc(G, &G->d_pos, 4) == hipSuccess && galloc(G, &G->d_rot, 2 * 2 * (size_t)c.layers * maxhd) == hipSuccess &&
+             hipHostMalloc((void**)&G->h_step, 8, 0) == hipSuccess &&
+             hipHostMalloc((void**)&G->h_rot, 2 * 2 * (size_t)c.layers * maxhd, 0) == hipSuccess;
+        if (!ok) return bail(gfail(err, err_len, "device allocation failed", RIBN_ERR_DEVICE));
+    }
     G->host_cs.assign((size_t)c.layers * R * maxhd, 0);
     G->host_sn.assign((size_t)c.layers * R * maxhd, 0);
     // decoder scales (decoder.rs:78-95)
@@ -651,13 +775,30 @@ namespace ribn {
 namespace {
 
 hipError_t project(ribn_rocm_gemma* G, const uint16_t* x, int rows, int ldx, const Mat& w, uint16_t* y, int ldy) {
+    if (rows <= 4 && w.n % 8 == 0 && w.k % 8 == 0 && w.k <= 4096 && ldx % 8 == 0) {
+        int C = 64;
+        while (C > 8 && (size_t)w.k * C > 32768) C >>= 1;
+        if (rows * C <= 256 && rows * (w.k / 8) <= 2048 && (size_t)w.k * C <= 32768) {
+            const size_t lds = ((size_t)C * (w.k + 1) + 3) / 4 * 16 + (size_t)rows * w.k * 4;
+            static bool raised = false;   // the slab and rows can exceed 64 KB of LDS
+            if (!raised) {
+                const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&project_cols_kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                if (e != hipSuccess) return e;
+                raised = true;
+            }
+            project_cols_kernel<<<(w.n + C - 1) / C, 256, lds, G->stream>>>(x, ldx, rows, w.t, w.k, w.n, C, y, ldy);
+            return hipGetLastError();
+        }
+    }
     const dim3 grid((w.n + 255) / 256, rows);
     project_kernel<<<grid, 256, 2 * (size_t)w.k, G->stream>>>(x, ldx, w.t, w.k, w.n, y, ldy);
     return hipGetLastError();
 }
 hipError_t rms(ribn_rocm_gemma* G, const uint16_t* x, int rows, int width, int ldx, const uint16_t* scale, uint16_t* y,
-               int ldy) {
-    rms_kernel<<<rows, 256, 0, G->stream>>>(x, ldx, width, G->c.eps, scale, y, ldy);
+               int ldy, const int* dpos = nullptr, size_t ypos = 0) {
+    if (width > 16000) return hipErrorInvalidValue;   // squares staged in LDS
+    rms_kernel<<<rows, 256, 4 * ((size_t)width + 1), G->stream>>>(x, ldx, width, G->c.eps, scale, y, ldy, dpos, ypos);
     return hipGetLastError();
 }
 hipError_t ew(ribn_rocm_gemma* G, int op, const uint16_t* a, const uint16_t* b, size_t n, float f, uint16_t* out) {
@@ -665,34 +806,15 @@ hipError_t ew(ribn_rocm_gemma* G, int op, const uint16_t* a, const uint16_t* b, 
     return hipGetLastError();
 }
 
-// one chunk of at most max_rows rows at the decoder's position (decoder.rs:334-409, 447-626)
-int gemma_chunk(ribn_rocm_gemma* G, const uint32_t* tokens, int n, bool last_logits, char* err, size_t err_len) {
+// rotary factors of every layer for positions p0 .. p0 + n - 1, on the host with
+// the C library's cosf/sinf as the reference (cpu/rotary.rs:33-81): row r of
+// layer l at cs / sn + l * fstride + r * head_dim
+void fill_rotary(const ribn_rocm_gemma* G, int p0, int n, uint16_t* cs_all, uint16_t* sn_all, size_t fstride) {
     const GemmaConfig& c = G->c;
-    const int H = c.hidden, P = c.ple, packed = c.layers * P, F = c.intermediate;
-    const int p0 = G->position;
-    GCHK(hipMemcpyAsync(G->tokens, tokens, 4 * (size_t)n, hipMemcpyHostToDevice, G->stream));
-    embed_kernel<<<dim3((H + 255) / 256, n), 256, 0, G->stream>>>(G->embed.rows, H, G->tokens, G->embed_scale, G->hidden);
-    GCHK(hipGetLastError());
-    embed_kernel<<<dim3((packed + 255) / 256, n), 256, 0, G->stream>>>(G->ple_embed, packed, G->tokens,
-                                                                      G->ple_embed_scale, G->identity);
-    GCHK(hipGetLastError());
-    GCHK(project(G, G->hidden, n, H, G->ple_proj, G->projection, packed));
-    GCHK(ew(G, EW_SCALE, G->projection, nullptr, (size_t)n * packed, G->ple_projection_scale, G->projection));
-    // per-layer inputs: rms over each layer's slice, then (context + token) / sqrt(2)
-    for (int l = 0; l < c.layers; l++) {
-        uint16_t* dst = G->per_layer + (size_t)l * n * P;
-        GCHK(rms(G, G->projection + (size_t)l * P, n, P, packed, G->ple_norm, G->pg, P));
-        ple_input_kernel<<<(n * P + 255) / 256, 256, 0, G->stream>>>(G->pg, G->identity + (size_t)l * P, packed, n, P,
-                                                                      dst);
-        GCHK(hipGetLastError());
-    }
-    // rotary factors of every layer for the chunk's positions, on the host with the
-    // C library's cosf/sinf as the reference (cpu/rotary.rs:33-81); one upload
-    const size_t fstride = (size_t)G->max_rows * G->maxhd;
     for (int l = 0; l < c.layers; l++) {
         const int hd = c.head_dim[l], half = hd / 2;
-        uint16_t* cs = G->host_cs.data() + (size_t)l * fstride;
-        uint16_t* sn = G->host_sn.data() + (size_t)l * fstride;
+        uint16_t* cs = cs_all + (size_t)l * fstride;
+        uint16_t* sn = sn_all + (size_t)l * fstride;
         for (int r = 0; r < n; r++) {
             const float position = (float)(p0 + r);
             for (int p = 0; p < half; p++) {
@@ -703,61 +825,141 @@ int gemma_chunk(ribn_rocm_gemma* G, const uint32_t* tokens, int n, bool last_log
             }
         }
     }
-    GCHK(hipMemcpyAsync(G->cosine, G->host_cs.data(), 2 * G->host_cs.size(), hipMemcpyHostToDevice, G->stream));
-    GCHK(hipMemcpyAsync(G->sine, G->host_sn.data(), 2 * G->host_sn.size(), hipMemcpyHostToDevice, G->stream));
+}
+
+// The launches of one chunk of n rows (decoder.rs:334-409, 447-626), tokens in
+// G->tokens and rotary factors at cos_base / sin_base (layer l at + l * fstride).
+// dpos == nullptr: the chunk starts at the host position G->position. Otherwise
+// the chunk is one decode row at the position in device memory *dpos (graph
+// replays: every launch argument is then the same at every position).
+hipError_t chunk_body(ribn_rocm_gemma* G, int n, bool last_logits, const int* dpos, const uint16_t* cos_base,
+                      const uint16_t* sin_base, size_t fstride) {
+    const GemmaConfig& c = G->c;
+    const int H = c.hidden, P = c.ple, packed = c.layers * P, F = c.intermediate;
+    const int p0 = dpos ? 0 : G->position;
+    hipError_t e;
+#define GE(x) do { if ((e = (x)) != hipSuccess) return e; } while (0)
+    embed_kernel<<<dim3((H + 255) / 256, n), 256, 0, G->stream>>>(G->embed.rows, H, G->tokens, G->embed_scale, G->hidden);
+    GE(hipGetLastError());
+    embed_kernel<<<dim3((packed + 255) / 256, n), 256, 0, G->stream>>>(G->ple_embed, packed, G->tokens,
+                                                                      G->ple_embed_scale, G->identity);
+    GE(hipGetLastError());
+    GE(project(G, G->hidden, n, H, G->ple_proj, G->projection, packed));
+    GE(ew(G, EW_SCALE, G->projection, nullptr, (size_t)n * packed, G->ple_projection_scale, G->projection));
+    // per-layer inputs: rms over each layer's slice, then (context + token) / sqrt(2)
+    for (int l = 0; l < c.layers; l++) {
+        uint16_t* dst = G->per_layer + (size_t)l * n * P;
+        GE(rms(G, G->projection + (size_t)l * P, n, P, packed, G->ple_norm, G->pg, P));
+        ple_input_kernel<<<(n * P + 255) / 256, 256, 0, G->stream>>>(G->pg, G->identity + (size_t)l * P, packed, n, P,
+                                                                      dst);
+        GE(hipGetLastError());
+    }
     for (int l = 0; l < c.layers; l++) {
         const LayerW& w = G->layer[l];
         const int hd = c.head_dim[l], half = hd / 2, qw = c.heads * hd, kw = c.kv_heads * hd;
-        const uint16_t* cosine = G->cosine + (size_t)l * fstride;
-        const uint16_t* sine = G->sine + (size_t)l * fstride;
+        const uint16_t* cosine = cos_base + (size_t)l * fstride;
+        const uint16_t* sine = sin_base + (size_t)l * fstride;
         // attention block (decoder.rs:487-577)
-        GCHK(rms(G, G->hidden, n, H, H, w.input_norm, G->normed, H));
-        GCHK(project(G, G->normed, n, H, w.q, G->q, qw));
-        GCHK(rms(G, G->q, n * c.heads, hd, hd, w.q_norm, G->qn, hd));
+        GE(rms(G, G->hidden, n, H, H, w.input_norm, G->normed, H));
+        GE(project(G, G->normed, n, H, w.q, G->q, qw));
+        GE(rms(G, G->q, n * c.heads, hd, hd, w.q_norm, G->qn, hd));
         const unsigned rq = (unsigned)(((size_t)n * c.heads * half + 255) / 256);
-        rotary_kernel<<<rq, 256, 0, G->stream>>>(G->qn, n, c.heads, hd, cosine, sine, G->q);
-        GCHK(hipGetLastError());
+        rotary_kernel<<<rq, 256, 0, G->stream>>>(G->qn, n, c.heads, hd, cosine, sine, G->q, nullptr, 0);
+        GE(hipGetLastError());
         if (c.kv_owner[l] == l) {
-            GCHK(project(G, G->normed, n, H, w.k, G->kbuf, kw));
-            GCHK(rms(G, G->kbuf, n * c.kv_heads, hd, hd, w.k_norm, G->knbuf, hd));
+            GE(project(G, G->normed, n, H, w.k, G->kbuf, kw));
+            GE(rms(G, G->kbuf, n * c.kv_heads, hd, hd, w.k_norm, G->knbuf, hd));
             const unsigned rk = (unsigned)(((size_t)n * c.kv_heads * half + 255) / 256);
             rotary_kernel<<<rk, 256, 0, G->stream>>>(G->knbuf, n, c.kv_heads, hd, cosine, sine,
-                                                    G->keys[l] + (size_t)p0 * kw);
-            GCHK(hipGetLastError());
-            GCHK(project(G, G->normed, n, H, w.v, G->vbuf, kw));
-            GCHK(rms(G, G->vbuf, n * c.kv_heads, hd, hd, nullptr, G->values[l] + (size_t)p0 * kw, hd));
+                                                    G->keys[l] + (size_t)p0 * kw, dpos, (size_t)kw);
+            GE(hipGetLastError());
+            GE(project(G, G->normed, n, H, w.v, G->vbuf, kw));
+            GE(rms(G, G->vbuf, n * c.kv_heads, hd, hd, nullptr, G->values[l] + (size_t)p0 * kw, hd, dpos, (size_t)kw));
         }
-        const int owner = c.kv_owner[l], kv_seq = p0 + n;
-        attention_kernel<<<dim3(n, c.heads), 256, 4 * (size_t)kv_seq, G->stream>>>(
+        const int owner = c.kv_owner[l];
+        // LDS for every score: the chunk's own length, or the whole context for a replayed row
+        const int kv_seq = p0 + n, kv_lds = dpos ? c.context : kv_seq;
+        attention_kernel<<<dim3(n, c.heads), 256, 4 * (size_t)kv_lds, G->stream>>>(
             G->q, n, G->keys[owner], G->values[owner], kv_seq, c.heads, c.kv_heads, hd,
-            c.kind[l] == kSliding ? c.window : 0, p0, G->attended);
-        GCHK(hipGetLastError());
-        GCHK(project(G, G->attended, n, qw, w.o, G->proj, H));
-        GCHK(rms(G, G->proj, n, H, H, w.post_attn_norm, G->normed, H));
-        GCHK(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
+            c.kind[l] == kSliding ? c.window : 0, p0, G->attended, dpos);
+        GE(hipGetLastError());
+        GE(project(G, G->attended, n, qw, w.o, G->proj, H));
+        GE(rms(G, G->proj, n, H, H, w.post_attn_norm, G->normed, H));
+        GE(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
         // feed-forward block and per-layer input gate (decoder.rs:579-626)
-        GCHK(rms(G, G->hidden, n, H, H, w.pre_ffn_norm, G->normed, H));
-        GCHK(project(G, G->normed, n, H, w.gate, G->gate, F));
-        GCHK(project(G, G->normed, n, H, w.up, G->up, F));
-        GCHK(ew(G, EW_GELU, G->gate, nullptr, (size_t)n * F, 0.f, G->gate));
-        GCHK(ew(G, EW_MUL, G->gate, G->up, (size_t)n * F, 0.f, G->gate));
-        GCHK(project(G, G->gate, n, F, w.down, G->down, H));
-        GCHK(rms(G, G->down, n, H, H, w.post_ffn_norm, G->normed, H));
-        GCHK(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
-        GCHK(project(G, G->hidden, n, H, w.ple_gate, G->pg, P));
-        GCHK(ew(G, EW_GELU, G->pg, nullptr, (size_t)n * P, 0.f, G->pg));
-        GCHK(ew(G, EW_MUL, G->pg, G->per_layer + (size_t)l * n * P, (size_t)n * P, 0.f, G->pg));
-        GCHK(project(G, G->pg, n, P, w.ple_proj, G->down, H));
-        GCHK(rms(G, G->down, n, H, H, w.post_ple_norm, G->normed, H));
-        GCHK(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
-        GCHK(ew(G, EW_SCALE, G->hidden, nullptr, (size_t)n * H, w.layer_scalar, G->hidden));
+        GE(rms(G, G->hidden, n, H, H, w.pre_ffn_norm, G->normed, H));
+        GE(project(G, G->normed, n, H, w.gate, G->gate, F));
+        GE(project(G, G->normed, n, H, w.up, G->up, F));
+        GE(ew(G, EW_GELU, G->gate, nullptr, (size_t)n * F, 0.f, G->gate));
+        GE(ew(G, EW_MUL, G->gate, G->up, (size_t)n * F, 0.f, G->gate));
+        GE(project(G, G->gate, n, F, w.down, G->down, H));
+        GE(rms(G, G->down, n, H, H, w.post_ffn_norm, G->normed, H));
+        GE(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
+        GE(project(G, G->hidden, n, H, w.ple_gate, G->pg, P));
+        GE(ew(G, EW_GELU, G->pg, nullptr, (size_t)n * P, 0.f, G->pg));
+        GE(ew(G, EW_MUL, G->pg, G->per_layer + (size_t)l * n * P, (size_t)n * P, 0.f, G->pg));
+        GE(project(G, G->pg, n, P, w.ple_proj, G->down, H));
+        GE(rms(G, G->down, n, H, H, w.post_ple_norm, G->normed, H));
+        GE(ew(G, EW_ADD, G->hidden, G->normed, (size_t)n * H, 0.f, G->hidden));
+        GE(ew(G, EW_SCALE, G->hidden, nullptr, (size_t)n * H, w.layer_scalar, G->hidden));
     }
     if (last_logits) {   // project_logits (decoder.rs:411-430): final norm, tied head, soft cap
-        GCHK(rms(G, G->hidden + (size_t)(n - 1) * H, 1, H, H, G->final_norm, G->normed, H));
-        GCHK(project(G, G->normed, 1, H, G->embed, G->logits, c.vocab));
-        GCHK(ew(G, EW_SOFTCAP, G->logits, nullptr, (size_t)c.vocab, c.softcap, G->logits));
+        GE(rms(G, G->hidden + (size_t)(n - 1) * H, 1, H, H, G->final_norm, G->normed, H));
+        GE(project(G, G->normed, 1, H, G->embed, G->logits, c.vocab));
+        GE(ew(G, EW_SOFTCAP, G->logits, nullptr, (size_t)c.vocab, c.softcap, G->logits));
     }
+#undef GE
+    return hipSuccess;
+}
+
+// one chunk of at most max_rows rows at the decoder's position, launched directly
+int gemma_chunk(ribn_rocm_gemma* G, const uint32_t* tokens, int n, bool last_logits, char* err, size_t err_len) {
+    const size_t fstride = (size_t)G->max_rows * G->maxhd;
+    GCHK(hipMemcpyAsync(G->tokens, tokens, 4 * (size_t)n, hipMemcpyHostToDevice, G->stream));
+    fill_rotary(G, G->position, n, G->host_cs.data(), G->host_sn.data(), fstride);
+    GCHK(hipMemcpyAsync(G->cosine, G->host_cs.data(), 2 * G->host_cs.size(), hipMemcpyHostToDevice, G->stream));
+    GCHK(hipMemcpyAsync(G->sine, G->host_sn.data(), 2 * G->host_sn.size(), hipMemcpyHostToDevice, G->stream));
+    GCHK(chunk_body(G, n, last_logits, nullptr, G->cosine, G->sine, fstride));
     G->position += n;
+    return RIBN_OK;
+}
+
+bool gemma_eager() {
+    static const bool eager = [] {
+        const char* v = std::getenv("RIBN_ROCM_EAGER");
+        return v && v[0] == '1';
+    }();
+    return eager;
+}
+
+// One decode row replayed from a HIP graph: the token, the position and the
+// row's rotary factors go to device memory first (from pinned host memory),
+// then the captured launches of chunk_body run with every argument fixed.
+int gemma_decode_row(ribn_rocm_gemma* G, uint32_t token, char* err, size_t err_len) {
+    const GemmaConfig& c = G->c;
+    G->h_step[0] = token;
+    G->h_step[1] = (uint32_t)G->position;
+    fill_rotary(G, G->position, 1, G->h_rot, G->h_rot + (size_t)c.layers * G->maxhd, (size_t)G->maxhd);
+    GCHK(hipMemcpyAsync(G->tokens, &G->h_step[0], 4, hipMemcpyHostToDevice, G->stream));
+    GCHK(hipMemcpyAsync(G->d_pos, &G->h_step[1], 4, hipMemcpyHostToDevice, G->stream));
+    GCHK(hipMemcpyAsync(G->d_rot, G->h_rot, 2 * 2 * (size_t)c.layers * G->maxhd, hipMemcpyHostToDevice, G->stream));
+    if (!G->decode_graph) {
+        hipGraph_t g = nullptr;
+        GCHK(hipStreamBeginCapture(G->stream, hipStreamCaptureModeThreadLocal));
+        const hipError_t e2 = chunk_body(G, 1, true, G->d_pos, G->d_rot, G->d_rot + (size_t)c.layers * G->maxhd,
+                                         (size_t)G->maxhd);
+        const hipError_t e = hipStreamEndCapture(G->stream, &g);
+        if (e2 != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            GCHK(e2);
+        }
+        GCHK(e);
+        const hipError_t e3 = hipGraphInstantiate(&G->decode_graph, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        GCHK(e3);
+    }
+    GCHK(hipGraphLaunch(G->decode_graph, G->stream));
+    G->position += 1;
     return RIBN_OK;
 }
 
@@ -772,6 +974,13 @@ int gemma_step(ribn_rocm_gemma* G, const uint32_t* tokens, uint32_t n, uint16_t*
         if (tokens[i] >= (uint32_t)c.vocab)
             return gfail(err, err_len, "empty, overlong or out-of-range token chunk", RIBN_ERR_INVALID);
     GCHK(hipSetDevice(G->device));
+    if (n == 1 && logits && G->d_pos && !gemma_eager()) {
+        int rc = gemma_decode_row(G, tokens[0], err, err_len);
+        if (rc != RIBN_OK) return rc;
+        GCHK(hipMemcpyAsync(logits, G->logits, 2 * (size_t)c.vocab, hipMemcpyDeviceToHost, G->stream));
+        GCHK(hipStreamSynchronize(G->stream));
+        return RIBN_OK;
+    }
     // rows beyond max_rows run as consecutive sub-chunks (prefill equals serial)
     for (uint32_t done = 0; done < n;) {
         const int m = (int)std::min<uint32_t>(n - done, (uint32_t)G->max_rows);
