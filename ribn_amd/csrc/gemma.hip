@@ -780,12 +780,10 @@ hipError_t project(ribn_rocm_gemma* G, const uint16_t* x, int rows, int ldx, con
         while (C > 8 && (size_t)w.k * C > 32768) C >>= 1;
         if (rows * C <= 256 && rows * (w.k / 8) <= 2048 && (size_t)w.k * C <= 32768) {
             const size_t lds = ((size_t)C * (w.k + 1) + 3) / 4 * 16 + (size_t)rows * w.k * 4;
-            static bool raised = false;   // the slab and rows can exceed 64 KB of LDS
-            if (!raised) {
+            if (lds > 65536) {   // the slab and rows can exceed 64 KB of LDS (per device: every launch)
                 const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&project_cols_kernel),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
                 if (e != hipSuccess) return e;
-                raised = true;
             }
             project_cols_kernel<<<(w.n + C - 1) / C, 256, lds, G->stream>>>(x, ldx, rows, w.t, w.k, w.n, C, y, ldy);
             return hipGetLastError();

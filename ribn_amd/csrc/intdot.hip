@@ -432,12 +432,10 @@ size_t intdot_lds(const IdArgs& p) {
 
 template <int TA, int TB, int MODE, int MB>
 hipError_t id_launch(const IdArgs& p, int n_wg, size_t lds, hipStream_t st) {
-    static bool raised = false;   // once per process: the attribute covers every later launch
-    if (!raised) {
+    if (lds > 65536) {   // per device, so on every launch that needs it
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&intdot_kernel<TA, TB, MODE, MB>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        raised = true;
     }
     intdot_kernel<TA, TB, MODE, MB><<<n_wg, kIdThreads, lds, st>>>(p);
     return hipGetLastError();
