@@ -151,6 +151,14 @@ struct WFrag<8> {
     uint32_t d16;
     u4v_t qv[2];
     __device__ static __forceinline__ int xoff(int ks, int j) { return 32 * j + 8 * ks; }
+    // K a multiple of the 128-wide tile: every block exists, no condition
+    __device__ __forceinline__ void fetch_full(const QMat& w, size_t row, int kt, int j) {
+        const size_t bi = row * w.nb + (size_t)(4 * kt + j);
+        d16 = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
+        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
+        qv[0] = qs[0];
+        qv[1] = qs[1];
+    }
     __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
         const int qb = 4 * kt + j;
         d16 = 0u;
@@ -187,7 +195,7 @@ struct WFrag<8> {
 // B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
 // MT (128 or 32) is the workgroup's chunk rows: 32 for batched decode rows,
 // where a 128-row tile would mostly multiply padding.
-template <int T, int MT>
+template <int T, int MT, bool FULL>
 __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg& sg, int m0, int n0, int kt0, int kt1,
                                           int z, uint16_t* xs) {
     constexpr int MB = MT / 16;                // 16-row blocks of chunk rows
@@ -212,8 +220,14 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
             const int idx = j * kGemmThreads + tid;
             const int r = idx >> 4, c = idx & 15;
             const int col = kt * kTileK + c * 8;
-            xr[j] = u4v_t{0u, 0u, 0u, 0u};
-            if (m0 + r < g.m && col < g.k) xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
+            if constexpr (FULL) {
+                // every column is inside X; rows past the chunk re-read its last row (their
+                // outputs are not stored), so the load needs no condition
+                xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)min(m0 + r, g.m - 1) * g.k + col);
+            } else {
+                xr[j] = u4v_t{0u, 0u, 0u, 0u};
+                if (m0 + r < g.m && col < g.k) xr[j] = *reinterpret_cast<const u4v_t*>(g.x + (size_t)(m0 + r) * g.k + col);
+            }
         }
     };
     auto store_x = [&](uint16_t* buf) {
@@ -225,17 +239,27 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
     };
     auto fetch_w = [&](WFrag<T> (&wf)[NB], int kt) {
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) wf[nb].fetch(sg.w, wrow[nb], kt, bj);
+        for (int nb = 0; nb < NB; nb++) {
+            if constexpr (FULL && T == 8) wf[nb].fetch_full(sg.w, wrow[nb], kt, bj);
+            else wf[nb].fetch(sg.w, wrow[nb], kt, bj);
+        }
     };
+    // FULL: the fetches of the next tiles are unconditional (past the last tile
+    // they re-read it), so the compiler can count the loads in flight behind each
+    // use and wait for exactly the ones it needs; under a condition it assumes
+    // none was issued and waits for all of them.
+    const int kt_last = kt1 - 1;
     if (kt0 < kt1) {
         fetch_x(kt0);
         fetch_w(w0, kt0);
         store_x(xs);
-        if (kt0 + 1 < kt1) fetch_x(kt0 + 1);
+        if (FULL) fetch_x(min(kt0 + 1, kt_last));
+        else if (kt0 + 1 < kt1) fetch_x(kt0 + 1);
         __syncthreads();
     }
     for (int kt = kt0; kt < kt1; kt++) {
-        if (kt + 1 < kt1) fetch_w(w1, kt + 1);
+        if (FULL) fetch_w(w1, min(kt + 1, kt_last));
+        else if (kt + 1 < kt1) fetch_w(w1, kt + 1);
         const uint16_t* xb = xs + (size_t)((kt - kt0) & 1) * MT * kLdsRow;
 #pragma unroll
         for (int ks = 0; ks < kTileK / 32; ks++) {
@@ -250,8 +274,14 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
                 for (int mb = 0; mb < MB; mb++) acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mb], b, acc[mb][nb], 0, 0, 0);
             }
         }
-        if (kt + 1 < kt1) {
+        if (FULL) {
             // the other buffer was last read in the previous tile, before its barrier
+            // (after the last tile it is not read again)
+            store_x(xs + (size_t)((kt + 1 - kt0) & 1) * MT * kLdsRow);
+            fetch_x(min(kt + 2, kt_last));
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) w0[nb] = w1[nb];
+        } else if (kt + 1 < kt1) {
             store_x(xs + (size_t)((kt + 1 - kt0) & 1) * MT * kLdsRow);
             if (kt + 2 < kt1) fetch_x(kt + 2);
 #pragma unroll
@@ -293,11 +323,19 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     const int n_kt = (g.k + kTileK - 1) / kTileK;
     const int ks = max(1, g.ksplit), z = blockIdx.z;
     const int kt0 = (int)((long)n_kt * z / ks), kt1 = (int)((long)n_kt * (z + 1) / ks);
+    // Unconditional fetches with exact waits pay at 32-row tiles (batched decode
+    // rows: configs[3] decode phase 4.24k -> 4.47k tok/s) and cost at 128-row
+    // tiles (512-token prefill 27.2k -> 23.4k tok/s), so only the former use them.
+    if (MT != 32 || g.k % kTileK) {   // uniform: a partial last K tile needs the conditional fetches
+        if (si == 2 && TB != TA) gemm_tile<TB, MT, false>(g, sg, m0, n0, kt0, kt1, z, plds);
+        else gemm_tile<TA, MT, false>(g, sg, m0, n0, kt0, kt1, z, plds);
+        return;
+    }
     if constexpr (TA == TB) {
-        gemm_tile<TA, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
+        gemm_tile<TA, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
     } else {
-        if (si == 2) gemm_tile<TB, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
-        else gemm_tile<TA, MT>(g, sg, m0, n0, kt0, kt1, z, plds);
+        if (si == 2) gemm_tile<TB, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
+        else gemm_tile<TA, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
     }
 }
 
