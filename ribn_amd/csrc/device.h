@@ -846,30 +846,33 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     constexpr int VIT = CH / 4;
     const int bn = lane & 15, bj = lane >> 4;
     const int nblk = (n + 31) / 32;
+    // Every load is unconditional: a position past the split re-reads the split's
+    // last position (finite, written data; such positions are masked to -inf
+    // before the softmax and their v meets a zero weight), page 0 when the split
+    // is empty (then nothing is used). So the same loads are in flight behind each
+    // use in every iteration, and the compiler waits for the current block's
+    // loads only, not for the next block's prefetch.
+    const int nlast = n > 0 ? n - 1 : 0;
+    const int nmask = n > 0 ? -1 : 0;
     auto kv_load = [&](int blk, u4_t (&kr)[2][KC], u4_t (&vr)[VIT][2]) {
         const int b0 = blk * 32;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int tl = b0 + 16 * h + bn;
-            if (tl < n) {
-                const uint16_t* src =
-                    a.kcache + ((size_t)(pg[tl >> 4] * a.hkv + kvh) * kPageTokens + bn) * HD + bj * (HD / 4);
+            const int tc = min(b0 + 16 * h + bn, nlast);
+            const int page = pg[tc >> 4] & nmask;
+            const uint16_t* src = a.kcache + ((size_t)(page * a.hkv + kvh) * kPageTokens + (tc & 15)) * HD + bj * (HD / 4);
 #pragma unroll
-                for (int c = 0; c < KC; c++) kr[h][c] = *reinterpret_cast<const u4_t*>(src + 8 * c);
-            } else {
-#pragma unroll
-                for (int c = 0; c < KC; c++) kr[h][c] = u4_t{0u, 0u, 0u, 0u};
-            }
+            for (int c = 0; c < KC; c++) kr[h][c] = *reinterpret_cast<const u4_t*>(src + 8 * c);
         }
 #pragma unroll
         for (int it = 0; it < VIT; it++) {
             const int item = it * 64 + lane, pp = item / CH, c8 = item % CH;
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const int tl = b0 + 2 * pp + e;
-                vr[it][e] = tl < n ? *reinterpret_cast<const u4_t*>(
-                                         a.vcache + ((size_t)(pg[tl >> 4] * a.hkv + kvh) * kPageTokens + (tl & 15)) * HD + c8 * 8)
-                                   : u4_t{0u, 0u, 0u, 0u};
+                const int tc = min(b0 + 2 * pp + e, nlast);
+                const int page = pg[tc >> 4] & nmask;
+                vr[it][e] = *reinterpret_cast<const u4_t*>(
+                    a.vcache + ((size_t)(page * a.hkv + kvh) * kPageTokens + (tc & 15)) * HD + c8 * 8);
             }
         }
     };
