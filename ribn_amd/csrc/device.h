@@ -1024,9 +1024,9 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         // accesses in order; the compiler barriers keep that order in the code.
         if (wave < nblk) v_stage(wave, vr);
         asm volatile("" ::: "memory");
-        for (int blk = wave; blk < nblk; blk += kWaves) {   // wave-uniform
-            u4_t kn[2][KC], vn[VIT][2];
-            kv_load(blk + kWaves, kn, vn);
+        // One block's scores, softmax update and O^T accumulation (K in kr, V^T in
+        // the wave's LDS tile).
+        auto block = [&](int blk) {
             const int b0 = blk * 32;
             f4v_t st[2];
 #pragma unroll
@@ -1076,14 +1076,23 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 acc[db] *= alpha;
                 acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, va), pb, acc[db], 0, 0, 0);
             }
+        };
+        // Blocks with a successor in this wave prefetch it; the wave's last block
+        // issues no load, so nothing is left in flight behind its use.
+        int blk = wave;
+        for (; blk + kWaves < nblk; blk += kWaves) {   // wave-uniform
+            u4_t kn[2][KC], vn[VIT][2];
+            kv_load(blk + kWaves, kn, vn);
+            block(blk);
             asm volatile("" ::: "memory");
-            if (blk + kWaves < nblk) v_stage(blk + kWaves, vn);   // after this block's reads
+            v_stage(blk + kWaves, vn);   // after this block's reads
             asm volatile("" ::: "memory");
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int c = 0; c < KC; c++) kr[h][c] = kn[h][c];
         }
+        if (blk < nblk) block(blk);
         // -- merge the waves: per-head statistics, then O^T rows
         l_run = xor32_sum(xor16_sum(l_run));
         if (bj == 0 && bn < G) {
