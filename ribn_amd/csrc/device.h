@@ -563,12 +563,77 @@ __device__ __forceinline__ void mv_group(const Group<T>& g, const WaveWork& w, c
     }
 }
 
+// The input of an attention-output projection whose attention launch left its
+// split partials unmerged (AttnArgs::defer):
+//   x[h HD + d] = sum_s w_s o_s[h][d] / sum_s w_s l_s,  w_s = 2^(m_s - max_s m_s)
+// for query head h (KV head h / G); (o_s, m_s, l_s) is split s's record:
+// unnormalized output (binary16), base-2 score maximum, weight sum (m = -inf,
+// w = 0 for an empty split). The same log-sum-exp merge as the attention
+// launch's own. Each thread merges its group of 16 inputs in registers and
+// stages it as stage_x does; the first pass's loads are issued before the
+// weight loads (merge_issue), like stage_pre's, as loads complete in order.
+struct MergePre {
+    u4_t p[kDeferMaxSplits][2];
+    float m[kDeferMaxSplits], l[kDeferMaxSplits];
+};
+__device__ __forceinline__ void merge_issue(const MvArgs& a, int base, MergePre& mp) {
+    const int HD = a.parts_hd, G = a.parts_g, ns = a.parts_splits, rec = G * HD + 2 * G;
+    const int g = min(base + (int)threadIdx.x, a.k / 16 - 1);
+    const int h = 16 * g / HD, d = 16 * g % HD, j = h / G, gg = h % G;
+#pragma unroll
+    for (int s = 0; s < kDeferMaxSplits; s++) {
+        const float* r = a.parts + (size_t)(j * ns + min(s, ns - 1)) * rec;
+        const u4_t* q = reinterpret_cast<const u4_t*>(reinterpret_cast<const uint16_t*>(r) + gg * HD + d);
+        mp.p[s][0] = q[0];
+        mp.p[s][1] = q[1];
+        mp.m[s] = r[G * HD + gg];
+        mp.l[s] = r[G * HD + G + gg];
+    }
+}
+template <int T>
+__device__ __forceinline__ float stage_merged(const MvArgs& a, MergePre& mp, int8_t* xs, float* gs) {
+    const int ns = a.parts_splits, nt = (int)blockDim.x, n16 = a.k / 16;
+    const float4 ones[4] = {{1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}};
+    float ss = 0.f;
+    for (int base = 0; base < n16; base += nt) {   // uniform
+        if (base > 0) merge_issue(a, base, mp);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kDeferMaxSplits; s++)
+            if (s < ns) mx = fmaxf(mx, mp.m[s]);
+        float den = 0.f, o[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < kDeferMaxSplits; s++) {
+            const float w = s < ns && mp.m[s] != -INFINITY ? exp2f(mp.m[s] - mx) : 0.f;
+            den = fmaf(w, mp.l[s], den);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t word = dword_at(mp.p[s][e >> 2], e & 3);
+                o[2 * e] = fmaf(w, (float)__builtin_bit_cast(_Float16, (uint16_t)(word & 0xffffu)), o[2 * e]);
+                o[2 * e + 1] = fmaf(w, (float)__builtin_bit_cast(_Float16, (uint16_t)(word >> 16)), o[2 * e + 1]);
+            }
+        }
+        const float inv = 1.0f / den;
+        float4 xv[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xv[j] = float4{o[4 * j] * inv, o[4 * j + 1] * inv, o[4 * j + 2] * inv, o[4 * j + 3] * inv};
+        stage_group<T>(base + (int)threadIdx.x, a.k, xv, ones, false, xs, gs, ss);
+    }
+    __syncthreads();
+    return 1.0f;
+}
+
 // Ring of depth D for a wave with total >= D groups, after stage_x.
-template <int T, int MODE, int D, typename Sync>
+// MODE MV_ADD_MERGED: MV_ADD whose input is merged from attention partials (merge_parts).
+template <int T, int MODE_, int D, typename Sync>
 __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const WaveWork& w, int8_t* xs, float* gs,
                                         float* red, uint64_t& best, Sync&& sync) {
+    constexpr bool MERGE = MODE_ == MV_ADD_MERGED;
+    constexpr int MODE = MERGE ? MV_ADD : MODE_;
     const int total = w.n_items * w.ngr;
-    constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX;
+    constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX && !MERGE;
     // the residual launches (O, down) take a long input without norm: four passes
     // early (k up to 32768 at 512 threads). Their norm weights are a compile-time
     // null, so no staging pass holds a conditional load, whose wait would cover the
@@ -577,6 +642,8 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     const float* const norm_w = MODE == MV_ADD ? nullptr : a.norm_w;
     XPre<NP == 0 ? 1 : NP> pre;
     if constexpr (NP > 0) stage_pre<NP>(a.x, norm_w, a.k, pre);
+    MergePre mp;
+    if constexpr (MERGE) merge_issue(a, 0, mp);
     const float addend = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE) : 0.f;
     Group<T> ring[D];
     Cursor ld{0, 0};
@@ -590,7 +657,12 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     const float* const x = a.x;
     const float eps = a.eps;
     const int k = a.k;
-    const float oscale = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);
+    float oscale;
+    if constexpr (MERGE) {
+        oscale = stage_merged<T>(a, mp, xs, gs);
+    } else {
+        oscale = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);
+    }
     sync.mark();
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
     float a0 = 0.f, b0 = 0.f;
@@ -1125,19 +1197,38 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     sync.phase(6);
     const bool direct = a.n_splits == 1;
     float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD;
-        float o = 0.f;
+    if (a.defer && !direct) {
+        // records left for merge_parts hold the unnormalized output in binary16
+        // (pairs of values per word in the record's first G*HD/2 words): half the
+        // bytes for every workgroup of the projection that reads them all
+        uint32_t* rh = reinterpret_cast<uint32_t*>(rec);
+        for (int i2 = tid; i2 < G * HD / 2; i2 += kThreads) {
+            const int idx = 2 * i2, g = idx / HD;
+            float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) o = fmaf(L.wst[w][0][g], red[w][idx], o);
-        if (direct) st_agent(a.out + (size_t)kvh * G * HD + idx, o / stat[1][g]);
-        else st_agent(rec + idx, o);
+            for (int w = 0; w < kWaves; w++) {
+                o0 = fmaf(L.wst[w][0][g], red[w][idx], o0);
+                o1 = fmaf(L.wst[w][0][g], red[w][idx + 1], o1);
+            }
+            const _Float16 h0 = (_Float16)o0, h1 = (_Float16)o1;
+            st_agent(rh + i2, (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16));
+        }
+    } else {
+        for (int idx = tid; idx < G * HD; idx += kThreads) {
+            const int g = idx / HD;
+            float o = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) o = fmaf(L.wst[w][0][g], red[w][idx], o);
+            if (direct) st_agent(a.out + (size_t)kvh * G * HD + idx, o / stat[1][g]);
+            else st_agent(rec + idx, o);
+        }
     }
     if (direct) return true;
     if (tid < G) {
         st_agent(rec + G * HD + tid, n > 0 ? stat[0][tid] : -INFINITY);
         st_agent(rec + G * HD + G + tid, n > 0 ? stat[1][tid] : 0.f);
     }
+    if (a.defer) return true;   // the next launch merges the records (merge_parts)
     sync.phase(7);
     if (!arrive_last(a.counters + kvh, a.n_splits)) return true;
     sync.phase(8);

@@ -79,6 +79,7 @@ enum MvMode : int32_t {
     MV_ADD = 1,     // out[row] += y   (residual epilogue)
     MV_SILU = 2,    // pair (gate, up): out[j] = silu(gate_j) * up_j
     MV_HEAD = 3,    // vocab logits + greedy argmax (token written to the sequence)
+    MV_ADD_MERGED = 4,   // kernel variant of MV_ADD chosen for MvArgs::parts (not a host mode)
 };
 
 struct MvSeg {
@@ -111,7 +112,15 @@ struct MvArgs {
     MvSeg seg[3];
     HeadEpi head;
     const StepCtl* ctl;
+    // MV_ADD only, optional: x is the merge of decode attention's split partials
+    // (AttnArgs::defer), records [hkv][parts_splits][parts_g * parts_hd + 2 parts_g]
+    const float* parts;
+    int32_t parts_splits, parts_g, parts_hd;
 };
+
+// Largest split count whose partials the attention-output projection merges
+// itself (AttnArgs::defer); beyond it the attention launch merges them.
+constexpr int kDeferMaxSplits = 8;
 
 // Per-step rotary table: cos/sin of theta_p = pos * base^(-2p/rot) for the
 // active sequence's position, written by the embedding kernel.
@@ -137,6 +146,8 @@ struct AttnArgs {
     float* out;              // [hq][hd]
     const StepCtl* ctl;
     int32_t hq, hkv, hd, rot, n_splits, kv_f16;
+    int32_t defer;           // 1 < n_splits <= kDeferMaxSplits: leave the split partials in `part`
+                             // for the next matvec (MvArgs::parts) instead of merging them here
     float eps;
     float scale_log2;        // log2(e) / sqrt(hd)
 };

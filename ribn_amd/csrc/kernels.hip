@@ -287,9 +287,12 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
     if (a.waves != 0 && a.waves != 4 && a.waves != 8) return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; i++)   // per-row addends are held one per lane (mv_addend)
         if ((a.mode == MV_ADD || a.seg[i].bias) && a.seg[i].ipw > 32) return hipErrorInvalidValue;
+    if (a.parts && (a.mode != MV_ADD || a.parts_splits < 2 || a.parts_splits > kDeferMaxSplits || a.parts_g < 1 ||
+                    a.parts_hd < 16 || a.parts_hd % 16 || a.k % (a.parts_hd * a.parts_g)))
+        return hipErrorInvalidValue;
     switch (a.mode) {
     case MV_STORE: return matvec_dispatch<MV_STORE>(a, n_wg, st);
-    case MV_ADD: return matvec_dispatch<MV_ADD>(a, n_wg, st);
+    case MV_ADD: return a.parts ? matvec_dispatch<MV_ADD_MERGED>(a, n_wg, st) : matvec_dispatch<MV_ADD>(a, n_wg, st);
     case MV_SILU: return matvec_dispatch<MV_SILU>(a, n_wg, st);
     case MV_HEAD: return matvec_dispatch<MV_HEAD>(a, n_wg, st);
     default: return hipErrorInvalidValue;
@@ -299,6 +302,7 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.n_splits < 1 || a.n_splits > kMaxSplits || a.hkv < 1 || a.hq % a.hkv || a.rot > a.hd || a.rot % 2)
         return hipErrorInvalidValue;
+    if (a.defer && a.n_splits > kDeferMaxSplits) return hipErrorInvalidValue;
     if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
     if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
     if (a.hd == 256) return a.kv_f16 ? attention_dispatch<256, true>(a, st) : attention_dispatch<256, false>(a, st);

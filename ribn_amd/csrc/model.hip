@@ -646,6 +646,12 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
     if (trace && (e = hipMemcpyAsync(trace, M->h, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st)) != hipSuccess)
         return e;
     AttnArgs at = attn_args(M, 0, n_splits);
+    // At a few splits (short contexts, where the launch is latency-bound) the
+    // o projection merges the attention's split partials while it stages its
+    // input, which saves the attention launch its arrival count and merge round
+    // trips. Gated attention multiplies the merged output first, so hybrids merge
+    // in the attention launch.
+    const bool defer = !M->hybrid && n_splits > 1 && n_splits <= kDeferMaxSplits;
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
         if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
@@ -654,10 +660,18 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
         } else {
             if (M->hybrid && (e = launch_matvec(M->mv_aux[l], M->wg_aux[l], st)) != hipSuccess) return e;
             at = attn_args(M, l, n_splits);
+            at.defer = defer ? 1 : 0;
             if ((e = launch_attention(at, st)) != hipSuccess) return e;
             if (M->hybrid && (e = launch_gate_mul(M->attn, M->att_gate, M->hq * M->hd, st)) != hipSuccess) return e;
         }
-        if ((e = launch_matvec(M->mv_o[l], M->wg_o[l], st)) != hipSuccess) return e;
+        MvArgs o = M->mv_o[l];
+        if (defer && !y.recurrent) {
+            o.parts = M->part;
+            o.parts_splits = n_splits;
+            o.parts_g = M->hq / M->hkv;
+            o.parts_hd = M->hd;
+        }
+        if ((e = launch_matvec(o, M->wg_o[l], st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st)) != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_down[l], M->wg_down[l], st)) != hipSuccess) return e;
         if (trace &&
