@@ -82,12 +82,19 @@ struct WFrag<12> {
     uint32_t dd, s;
     u4v_t qv;
     __device__ static __forceinline__ int xoff(int ks, int j) { return 64 * (j >> 1) + 16 * (j & 1) + 8 * (ks & 1) + 32 * (ks >> 1); }
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
-        const size_t bi = row * w.nb + (kt >> 1);
-        const int p = 2 * (kt & 1) + (j >> 1);
-        dd = *reinterpret_cast<const uint32_t*>(w.c + bi * 4);
-        s = reinterpret_cast<const uint32_t*>(w.b + bi * 16)[p];
-        qv = *reinterpret_cast<const u4v_t*>(w.a + bi * 128 + 32 * p + 16 * (j & 1));
+    // the lane's byte offsets into the planes (fixed over K); each fetch adds
+    // them to plane bases that depend on the K tile only (wave-uniform), so the
+    // loads take scalar-base + vector-offset addressing with no address math
+    struct Off { uint32_t a, b, c; };
+    __device__ static __forceinline__ Off lane_off(const QMat& w, size_t row, int j) {
+        const uint32_t rb = (uint32_t)(row * w.nb);
+        return Off{rb * 128u + 32u * (uint32_t)(j >> 1) + 16u * (uint32_t)(j & 1), rb * 16u + 4u * (uint32_t)(j >> 1), rb * 4u};
+    }
+    __device__ __forceinline__ void fetch(const QMat& w, const Off& o, int kt) {
+        const int kb = kt >> 1, h = kt & 1;
+        dd = *reinterpret_cast<const uint32_t*>(w.c + (size_t)kb * 4 + o.c);
+        s = *reinterpret_cast<const uint32_t*>(w.b + (size_t)kb * 16 + 8 * h + o.b);
+        qv = *reinterpret_cast<const u4v_t*>(w.a + (size_t)kb * 128 + 64 * h + o.a);
     }
     // value = round16(fma(q, sc*d, -m*dmin)): g * q is exact in fp32 (d has
     // 11 significant bits, sc 6, q 4), so the fma rounds once, as the
@@ -117,16 +124,21 @@ struct WFrag<14> {
     uint32_t d16, sc01, sc23;   // scale bytes (v=0, v=2) and (v=1, v=3)
     uint2 ql0, ql1, qh;
     __device__ static __forceinline__ int xoff(int ks, int j) { return 32 * ks + 8 * j; }
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
-        const size_t bi = row * w.nb + (kt >> 1);
-        const int h = kt & 1;
-        d16 = *reinterpret_cast<const uint16_t*>(w.d + bi * 2);
-        const uint8_t* sp = w.c + bi * 16 + 8 * h + 2 * (j >> 1);
+    struct Off { uint32_t a, b, c, d; };
+    __device__ static __forceinline__ Off lane_off(const QMat& w, size_t row, int j) {
+        const uint32_t rb = (uint32_t)(row * w.nb);
+        return Off{rb * 128u + 8u * (uint32_t)j, rb * 64u + 8u * (uint32_t)j, rb * 16u + 2u * (uint32_t)(j >> 1), rb * 2u};
+    }
+    __device__ __forceinline__ void fetch(const QMat& w, const Off& o, int kt) {
+        const int kb = kt >> 1, h = kt & 1;
+        d16 = *reinterpret_cast<const uint16_t*>(w.d + (size_t)kb * 2 + o.d);
+        const uint8_t* sp = w.c + (size_t)kb * 16 + 8 * h + o.c;
         sc01 = *reinterpret_cast<const uint16_t*>(sp);
         sc23 = *reinterpret_cast<const uint16_t*>(sp + 4);
-        ql0 = *reinterpret_cast<const uint2*>(w.a + bi * 128 + 64 * h + 8 * j);
-        ql1 = *reinterpret_cast<const uint2*>(w.a + bi * 128 + 64 * h + 32 + 8 * j);
-        qh = *reinterpret_cast<const uint2*>(w.b + bi * 64 + 32 * h + 8 * j);
+        const uint8_t* ap = w.a + (size_t)kb * 128 + 64 * h + o.a;
+        ql0 = *reinterpret_cast<const uint2*>(ap);
+        ql1 = *reinterpret_cast<const uint2*>(ap + 32);
+        qh = *reinterpret_cast<const uint2*>(w.b + (size_t)kb * 64 + 32 * h + o.b);
     }
     // value = round16(round32(d*sc * (q - 32))), q - 32 exact in binary16
     __device__ __forceinline__ h8_t frag(int v) const {
@@ -151,25 +163,21 @@ struct WFrag<8> {
     uint32_t d16;
     u4v_t qv[2];
     __device__ static __forceinline__ int xoff(int ks, int j) { return 32 * j + 8 * ks; }
+    struct Off { uint32_t blk; int j; };   // block index of the lane's row and K slot
+    __device__ static __forceinline__ Off lane_off(const QMat& w, size_t row, int j) {
+        return Off{(uint32_t)(row * w.nb) + (uint32_t)j, j};
+    }
     // K a multiple of the 128-wide tile: every block exists, no condition
-    __device__ __forceinline__ void fetch_full(const QMat& w, size_t row, int kt, int j) {
-        const size_t bi = row * w.nb + (size_t)(4 * kt + j);
-        d16 = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
-        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
+    __device__ __forceinline__ void fetch_full(const QMat& w, const Off& o, int kt) {
+        d16 = *reinterpret_cast<const uint16_t*>(w.b + (size_t)kt * 8 + o.blk * 2u);
+        const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + (size_t)kt * 128 + o.blk * 32u);
         qv[0] = qs[0];
         qv[1] = qs[1];
     }
-    __device__ __forceinline__ void fetch(const QMat& w, size_t row, int kt, int j) {
-        const int qb = 4 * kt + j;
+    __device__ __forceinline__ void fetch(const QMat& w, const Off& o, int kt) {
         d16 = 0u;
         qv[0] = qv[1] = u4v_t{0u, 0u, 0u, 0u};
-        if (qb < (int)w.nb) {
-            const size_t bi = row * w.nb + (size_t)qb;
-            d16 = *reinterpret_cast<const uint16_t*>(w.b + bi * 2);
-            const u4v_t* qs = reinterpret_cast<const u4v_t*>(w.a + bi * 32);
-            qv[0] = qs[0];
-            qv[1] = qs[1];
-        }
+        if (4 * kt + o.j < (int)w.nb) fetch_full(w, o, kt);
     }
     // value = round16(d * q) (d * q is exact in fp32), q exact in binary16
     // (int8 as q + 128 unsigned)
@@ -209,9 +217,10 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
     for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) acc[i][nb] = f4_t{0.f, 0.f, 0.f, 0.f};
-    size_t wrow[NB];
+    typename WFrag<T>::Off woff[NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++) wrow[nb] = (size_t)min(n0 + 16 * NB * wave + 16 * nb + bn, n_rows - 1);
+    for (int nb = 0; nb < NB; nb++)
+        woff[nb] = WFrag<T>::lane_off(sg.w, (size_t)min(n0 + 16 * NB * wave + 16 * nb + bn, n_rows - 1), bj);
     u4v_t xr[XR];
     WFrag<T> w0[NB], w1[NB];   // raw weight bytes of tiles kt and kt + 1
     auto fetch_x = [&](int kt) {
@@ -240,8 +249,8 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
     auto fetch_w = [&](WFrag<T> (&wf)[NB], int kt) {
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
-            if constexpr (FULL && T == 8) wf[nb].fetch_full(sg.w, wrow[nb], kt, bj);
-            else wf[nb].fetch(sg.w, wrow[nb], kt, bj);
+            if constexpr (FULL && T == 8) wf[nb].fetch_full(sg.w, woff[nb], kt);
+            else wf[nb].fetch(sg.w, woff[nb], kt);
         }
     };
     // FULL: the fetches of the next tiles are unconditional (past the last tile
