@@ -492,74 +492,86 @@ struct Cursor {
 // loaded before the wave's first weight loads so that its latency overlaps
 // them: lane 2i holds item i's first row, lane 2i+1 its second (a gate/up
 // item's single row in lane 2i). Needs at most 32 items per wave.
-__device__ __forceinline__ float mv_addend(const MvSeg& sg, const WaveWork& w, int mode) {
+__device__ __forceinline__ float mv_addend(const MvSeg& sg, const WaveWork& w, int mode, size_t roff = 0) {
     const int lane = threadIdx.x & 63;
     float v = 0.f;
     if (lane < 2 * w.n_items) {
         const int item = w.first_item + (lane >> 1) * w.stride;
         const int row = w.pair ? item : 2 * item + (lane & 1);
         if (row < w.n_rows && !(w.pair && (lane & 1))) {
-            if (mode == MV_ADD) v = sg.res[row];
+            if (mode == MV_ADD) v = sg.res[roff + row];
             if (sg.bias) v += sg.bias[row];
         }
     }
     return v;
 }
 
-template <int T, int MODE>
-__device__ __forceinline__ void mv_finish(const MvSeg& sg, const WaveWork& w, const Cursor& c, float& a0, float& b0,
-                                          float oscale, float addend, uint64_t& best) {
+template <int T, int MODE, int R>
+__device__ __forceinline__ void mv_finish(const MvSeg& sg, const WaveWork& w, const Cursor& c, float (&a0)[R],
+                                          float (&b0)[R], const float (&oscale)[R], const float (&addend)[R],
+                                          uint64_t& best, size_t ldo) {
     if (c.gi != w.ngr - 1) return;
     const int lane = threadIdx.x & 63;
-    // both row sums in one reduction: the permlane32 swap of (a0, b0) leaves
-    // {a0[l], a0[l + 32]} in lanes 0-31 and {b0[l - 32], b0[l]} in lanes 32-63,
-    // then DPP sums within each half
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0), __float_as_uint(b0), false, false);
-    float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    v = xor16_sum(group_sum<16>(v));
-    const float ya = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) * oscale;
-    const float yb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) * oscale;
-    a0 = b0 = 0.f;
     const int item = w.first_item + c.it * w.stride;
     const int ra = w.pair ? item : 2 * item;
     const int rb = w.pair ? item : ra + 1;
     // (the host keeps a launch with addends at <= 32 items per wave)
     const int al = (2 * c.it) & 63;
-    const float add_a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend), al));
-    const float add_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend), al + 1));
-    if (lane == 0) {
-        const bool has_b = !w.pair && rb < w.n_rows;
-        // outputs are written through to memory (agent-scope stores) so
-        // workgroups on other XCDs read them after a grid barrier
-        if constexpr (MODE == MV_ADD) {
-            st_agent(sg.out + ra, add_a + ya);
-            if (has_b) st_agent(sg.out + rb, add_b + yb);
-        } else if constexpr (MODE == MV_SILU) {
-            st_agent(sg.out + ra, ya / (1.0f + expf(-ya)) * yb);
-        } else {
-            const float oa = ya + add_a, ob = yb + add_b;
-            st_agent(sg.out + ra, oa);
-            if (has_b) st_agent(sg.out + rb, ob);
-            if constexpr (MODE == MV_HEAD) {
-                best = max(best, argmax_key(oa, (uint32_t)ra));
-                if (has_b) best = max(best, argmax_key(ob, (uint32_t)rb));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        // both row sums in one reduction: the permlane32 swap of (a0, b0) leaves
+        // {a0[l], a0[l + 32]} in lanes 0-31 and {b0[l - 32], b0[l]} in lanes 32-63,
+        // then DPP sums within each half
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0[r]), __float_as_uint(b0[r]), false, false);
+        float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        v = xor16_sum(group_sum<16>(v));
+        const float ya = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) * oscale[r];
+        const float yb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) * oscale[r];
+        a0[r] = b0[r] = 0.f;
+        const float add_a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend[r]), al));
+        const float add_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(addend[r]), al + 1));
+        float* const out = sg.out + (size_t)r * ldo;
+        if (lane == 0) {
+            const bool has_b = !w.pair && rb < w.n_rows;
+            // outputs are written through to memory (agent-scope stores) so
+            // workgroups on other XCDs read them after a grid barrier
+            if constexpr (MODE == MV_ADD) {
+                st_agent(out + ra, add_a + ya);
+                if (has_b) st_agent(out + rb, add_b + yb);
+            } else if constexpr (MODE == MV_SILU) {
+                st_agent(out + ra, ya / (1.0f + expf(-ya)) * yb);
+            } else {
+                const float oa = ya + add_a, ob = yb + add_b;
+                st_agent(out + ra, oa);
+                if (has_b) st_agent(out + rb, ob);
+                if constexpr (MODE == MV_HEAD) {
+                    static_assert(R == 1, "the head's argmax epilogue takes one row");
+                    best = max(best, argmax_key(oa, (uint32_t)ra));
+                    if (has_b) best = max(best, argmax_key(ob, (uint32_t)rb));
+                }
             }
         }
     }
 }
 
-template <int T>
+// R input rows staged rb bytes apart: each weight unit is applied to every row.
+template <int T, int R>
 __device__ __forceinline__ void mv_group(const Group<T>& g, const WaveWork& w, const Cursor& c, const u4_t* xs4,
-                                         const float* gs, float& a0, float& b0) {
+                                         const float* gs, size_t rb, float (&a0)[R], float (&b0)[R]) {
     using U = Unit<T>;
     const int u0 = c.gi * 128 + (threadIdx.x & 63), u1 = u0 + 64;
-    if (u0 < w.n_units) {
-        a0 = U::apply(g.a0, u0, xs4, w.n_units, gs, a0);
-        b0 = U::apply(g.b0, u0, xs4, w.n_units, gs, b0);
-    }
-    if (u1 < w.n_units) {
-        a0 = U::apply(g.a1, u1, xs4, w.n_units, gs, a0);
-        b0 = U::apply(g.b1, u1, xs4, w.n_units, gs, b0);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const u4_t* x4 = reinterpret_cast<const u4_t*>(reinterpret_cast<const uint8_t*>(xs4) + r * rb);
+        const float* gr = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(gs) + r * rb);
+        if (u0 < w.n_units) {
+            a0[r] = U::apply(g.a0, u0, x4, w.n_units, gr, a0[r]);
+            b0[r] = U::apply(g.b0, u0, x4, w.n_units, gr, b0[r]);
+        }
+        if (u1 < w.n_units) {
+            a0[r] = U::apply(g.a1, u1, x4, w.n_units, gr, a0[r]);
+            b0[r] = U::apply(g.b1, u1, x4, w.n_units, gr, b0[r]);
+        }
     }
 }
 
@@ -627,10 +639,14 @@ __device__ __forceinline__ float stage_merged(const MvArgs& a, MergePre& mp, int
 
 // Ring of depth D for a wave with total >= D groups, after stage_x.
 // MODE MV_ADD_MERGED: MV_ADD whose input is merged from attention partials (merge_parts).
-template <int T, int MODE_, int D, typename Sync>
+// R > 1: R input rows (MvArgs::rows, ldx floats apart) staged rb bytes apart in
+// LDS, outputs (and residuals) ldo floats apart; each weight unit is loaded
+// once and applied to every row.
+template <int T, int MODE_, int D, int R, typename Sync>
 __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const WaveWork& w, int8_t* xs, float* gs,
-                                        float* red, uint64_t& best, Sync&& sync) {
+                                        float* red, size_t rb, uint64_t& best, Sync&& sync) {
     constexpr bool MERGE = MODE_ == MV_ADD_MERGED;
+    static_assert(R == 1 || !MERGE, "merged attention partials take one row");
     constexpr int MODE = MERGE ? MV_ADD : MODE_;
     const int total = w.n_items * w.ngr;
     constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX && !MERGE;
@@ -644,7 +660,9 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     if constexpr (NP > 0) stage_pre<NP>(a.x, norm_w, a.k, pre);
     MergePre mp;
     if constexpr (MERGE) merge_issue(a, 0, mp);
-    const float addend = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE) : 0.f;
+    float addend[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) addend[r] = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE, (size_t)r * a.ldo) : 0.f;
     Group<T> ring[D];
     Cursor ld{0, 0};
 #pragma unroll
@@ -657,35 +675,41 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     const float* const x = a.x;
     const float eps = a.eps;
     const int k = a.k;
-    float oscale;
+    float oscale[R];
     if constexpr (MERGE) {
-        oscale = stage_merged<T>(a, mp, xs, gs);
+        oscale[0] = stage_merged<T>(a, mp, xs, gs);
     } else {
-        oscale = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);
+        oscale[0] = stage_x<T, NP>(x, norm_w, eps, k, xs, gs, red, &pre);
+#pragma unroll
+        for (int r = 1; r < R; r++)
+            oscale[r] = stage_x<T>(x + (size_t)r * a.ldx, norm_w, eps, k, xs + r * rb,
+                                   reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(gs) + r * rb), red);
     }
     sync.mark();
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
-    float a0 = 0.f, b0 = 0.f;
+    float a0[R], b0[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) a0[r] = b0[r] = 0.f;
     Cursor c{0, 0};
     int q0 = 0;
     for (; q0 + D < total; q0 += D) {
 #pragma unroll
         for (int j = 0; j < D; j++) {
-            mv_group<T>(ring[j], w, c, xs4, gs, a0, b0);
+            mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
             load_group<T>(ring[j], w, ld.it, ld.gi);
             if (ldq + 1 < total) {
                 ld.next(w.ngr);
                 ++ldq;
             }
-            mv_finish<T, MODE>(sg, w, c, a0, b0, oscale, addend, best);
+            mv_finish<T, MODE, R>(sg, w, c, a0, b0, oscale, addend, best, (size_t)a.ldo);
             c.next(w.ngr);
         }
     }
 #pragma unroll
     for (int j = 0; j < D; j++) {
         if (q0 + j < total) {
-            mv_group<T>(ring[j], w, c, xs4, gs, a0, b0);
-            mv_finish<T, MODE>(sg, w, c, a0, b0, oscale, addend, best);
+            mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
+            mv_finish<T, MODE, R>(sg, w, c, a0, b0, oscale, addend, best, (size_t)a.ldo);
             c.next(w.ngr);
         }
     }
@@ -696,26 +720,29 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
 // for a wave with fewer groups). The first loads are issued before `sync`
 // (a grid barrier in the persistent step, nothing in a standalone launch).
 // Returns false if sync reports a failed barrier.
-template <int T, int MODE, int P, typename Sync>
+template <int T, int MODE, int P, int R, typename Sync>
 __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWork& w, int8_t* xs, float* gs,
-                                       float* red, uint64_t& best, Sync&& sync) {
+                                       float* red, size_t rb, uint64_t& best, Sync&& sync) {
     w.n_units = (int)sg.w.nb * Unit<T>::kPerBlock;
     w.ngr = (w.n_units + 127) / 128;
     const int total = w.n_items * w.ngr;
     // depth: one that divides the wave's group count (no refill past the end),
     // or the full depth when the count is large enough for a few reloads of the
     // last group not to matter
-    if (total >= P && (total % P == 0 || total >= 3 * P)) return mv_ring<T, MODE, P>(a, sg, w, xs, gs, red, best, sync);
+    if (total >= P && (total % P == 0 || total >= 3 * P)) return mv_ring<T, MODE, P, R>(a, sg, w, xs, gs, red, rb, best, sync);
     if constexpr (P > 3) {
-        if (total >= 3 && total % 3 == 0) return mv_ring<T, MODE, 3>(a, sg, w, xs, gs, red, best, sync);
+        if (total >= 3 && total % 3 == 0) return mv_ring<T, MODE, 3, R>(a, sg, w, xs, gs, red, rb, best, sync);
     }
     if constexpr (P > 2) {
-        if (total >= 2) return mv_ring<T, MODE, 2>(a, sg, w, xs, gs, red, best, sync);
+        if (total >= 2) return mv_ring<T, MODE, 2, R>(a, sg, w, xs, gs, red, rb, best, sync);
     }
-    if (total >= 1) return mv_ring<T, MODE, 1>(a, sg, w, xs, gs, red, best, sync);
+    if (total >= 1) return mv_ring<T, MODE, 1, R>(a, sg, w, xs, gs, red, rb, best, sync);
     // no work: take part in the barrier and the workgroup's staging
     if (!sync()) return false;
-    stage_x<T>(a.x, a.norm_w, a.eps, a.k, xs, gs, red);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        stage_x<T>(a.x + (size_t)r * a.ldx, a.norm_w, a.eps, a.k, xs + r * rb,
+                   reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(gs) + r * rb), red);
     sync.mark();
     return true;
 }
@@ -729,11 +756,13 @@ struct NoSync {
 
 // One workgroup's share of a matvec launch laid out in `a` (segments, items per
 // wave). Workgroups beyond the layout only sync. LDS: staged input at `lds`.
-template <int TA, int TB, int MODE, int PA, int PB, typename Sync>
+// R > 1: R input rows (see mv_ring), staged mv_red_offset(k) bytes apart.
+template <int TA, int TB, int MODE, int PA, int PB, int R = 1, typename Sync>
 __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uint64_t& best, Sync&& sync) {
+    const size_t rb = mv_red_offset(a.k);
     int8_t* xs = reinterpret_cast<int8_t*>(lds);
     float* gs = reinterpret_cast<float*>(lds + (size_t)a.k * 2);
-    float* red = reinterpret_cast<float*>(lds + mv_red_offset(a.k));
+    float* red = reinterpret_cast<float*>(lds + R * rb);
     int si = 0;
     if (a.nseg > 1 && wg >= a.seg[1].wg_begin) si = 1;
     if (a.nseg > 2 && wg >= a.seg[2].wg_begin) si = 2;
@@ -754,8 +783,8 @@ __device__ __forceinline__ bool mv_wg(const MvArgs& a, int wg, uint8_t* lds, uin
     w.first_item = lwg * sg.ipw * nw + wave;
     const int n_item_total = pair ? w.n_rows : (w.n_rows + 1) / 2;
     w.n_items = max(0, min(sg.ipw, (n_item_total - w.first_item + nw - 1) / nw));
-    if (si == 2 && TB != TA) return mv_run<TB, MODE, PB>(a, sg, w, xs, gs, red, best, sync);
-    return mv_run<TA, MODE, PA>(a, sg, w, xs, gs, red, best, sync);
+    if (si == 2 && TB != TA) return mv_run<TB, MODE, PB, R>(a, sg, w, xs, gs, red, rb, best, sync);
+    return mv_run<TA, MODE, PA, R>(a, sg, w, xs, gs, red, rb, best, sync);
 }
 
 // Greedy token of the head launch: first maximum over the vocabulary, NaN

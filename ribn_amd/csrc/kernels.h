@@ -116,7 +116,12 @@ struct MvArgs {
     // (AttnArgs::defer), records [hkv][parts_splits][parts_g * parts_hd + 2 parts_g]
     const float* parts;
     int32_t parts_splits, parts_g, parts_hd;
+    // rows > 1 (up to kMvMaxRows; MV_STORE, MV_ADD, MV_SILU): that many input rows
+    // ldx floats apart, outputs and residuals ldo floats apart, each weight
+    // loaded once for all rows; 0 or 1: one row
+    int32_t rows, ldx, ldo;
 };
+constexpr int kMvMaxRows = 4;
 
 // Largest split count whose partials the attention-output projection merges
 // itself (AttnArgs::defer); beyond it the attention launch merges them.
@@ -273,8 +278,13 @@ hipError_t launch_gate_mul(float* x, const float* gate, int n, hipStream_t strea
 
 // Launchers (kernels.hip). All enqueue on `stream` and return hipSuccess or the launch error.
 hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t stream);
+// launch_matvec's rows > 1 case (matvec_rows.hip), after its checks
+hipError_t launch_matvec_rows(const MvArgs& a, int n_wg, hipStream_t stream);
 int matvec_rows_per_wg(const MvArgs& a);
-size_t matvec_lds_bytes(int k);
+size_t matvec_lds_bytes(int k, int rows = 1);
+// Most input rows one matvec launch takes for inputs of k values (staged rows
+// must fit the 160 KB of LDS), at most kMvMaxRows.
+int matvec_max_rows(int k);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 
 // Batched decode: one decode row per sequence, all in one step. Row r consumes

@@ -17,7 +17,7 @@
 // argmax (nvidia/src/model_ops.rs:203-260), dequant (gguf/src/lib.rs:577-649).
 #include <algorithm>
 
-#include "device.h"
+#include "matvec.h"
 
 namespace ribn {
 namespace {
@@ -65,34 +65,7 @@ __global__ void advance_kernel(const StepCtl* ctl) {
     if (threadIdx.x == 0) ctl->seq->pos += 1;
 }
 
-// Ring depth (load groups in flight per wave) of the standalone matvec, per type.
-// Under the one-workgroup-per-CU layout, the Q4_K gate/up launch measured 12.7 us
-// at depth 2, 13.3 us at depth 3 and 16.0 us at depth 6.
-#ifndef RIBN_RING_SA_Q4
-#define RIBN_RING_SA_Q4 2
-#endif
-#ifndef RIBN_RING_SA_Q6
-#define RIBN_RING_SA_Q6 3
-#endif
-#ifndef RIBN_RING_SA_Q8
-#define RIBN_RING_SA_Q8 3
-#endif
-template <int T>
-constexpr int ring_standalone() {
-    return T == 12 ? RIBN_RING_SA_Q4 : T == 14 ? RIBN_RING_SA_Q6 : RIBN_RING_SA_Q8;
-}
 
-// Fused dequant-matvec (gguf_gemv qwen_reference.rs:31-40; q*_gemv_warp
-// kernels/quantized/q4_k.cu:103, q6_k.cu:45, q8_0.cu:27). Each wave computes
-// two rows per item (or a gate/up pair); the first weight loads are issued
-// before the input is staged, so HBM streaming overlaps the prologue.
-template <int TA, int TB, int MODE>
-__global__ __launch_bounds__(kMaxMvThreads) void matvec_kernel(MvArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    uint64_t best = 0ull;
-    mv_wg<TA, TB, MODE, ring_standalone<TA>(), ring_standalone<TB>()>(a, blockIdx.x, lds, best, NoSync{});
-    if constexpr (MODE == MV_HEAD) head_finish(a, best, blockIdx.x, gridDim.x);
-}
 
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
@@ -252,33 +225,17 @@ hipError_t attention_dispatch(const AttnArgs& a, hipStream_t st) {
     }
 }
 
-int mv_waves(const MvArgs& a) { return a.waves ? a.waves : kWaves; }
-
-template <int MODE>
-hipError_t matvec_dispatch(const MvArgs& a, int n_wg, hipStream_t st) {
-    const size_t lds = matvec_lds_bytes(a.k);
-    const uint32_t ta = a.type_a, tb = a.nseg > 2 ? a.type_b : a.type_a;
-#define RIBN_MV(A, B)                                                                              \
-    if (ta == A && tb == B) {                                                                      \
-        if (lds > 65536) {                                                                         \
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_kernel<A, B, MODE>), \
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-            if (e != hipSuccess) return e;                                                         \
-        }                                                                                          \
-        matvec_kernel<A, B, MODE><<<n_wg, mv_waves(a) * 64, lds, st>>>(a);                                 \
-        return hipGetLastError();                                                                  \
-    }
-    if constexpr (MODE == MV_STORE) {
-        RIBN_MV(12, 14) RIBN_MV(14, 12) RIBN_MV(12, 8) RIBN_MV(8, 12) RIBN_MV(14, 8) RIBN_MV(8, 14)
-    }
-    RIBN_MV(12, 12) RIBN_MV(14, 14) RIBN_MV(8, 8)
-#undef RIBN_MV
-    return hipErrorInvalidValue;
-}
-
 }  // namespace
 
-size_t matvec_lds_bytes(int k) { return mv_red_offset(k) + 64 * 4; }
+size_t matvec_lds_bytes(int k, int rows) { return (size_t)std::max(rows, 1) * mv_red_offset(k) + 64 * 4; }
+
+constexpr size_t kLdsBytes = 160 * 1024;
+
+int matvec_max_rows(int k) {
+    int r = kMvMaxRows;
+    while (r > 1 && matvec_lds_bytes(k, r) > kLdsBytes) r--;
+    return r;
+}
 
 int matvec_rows_per_wg(const MvArgs& a) { return a.items_per_wave * mv_waves(a) * (a.mode == MV_SILU ? 1 : 2); }
 
@@ -290,6 +247,10 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
     if (a.parts && (a.mode != MV_ADD || a.parts_splits < 2 || a.parts_splits > kDeferMaxSplits || a.parts_g < 1 ||
                     a.parts_hd < 16 || a.parts_hd % 16 || a.k % (a.parts_hd * a.parts_g)))
         return hipErrorInvalidValue;
+    if (a.rows > 1) {
+        if (a.rows > matvec_max_rows(a.k) || a.parts || a.ldx < a.k) return hipErrorInvalidValue;
+        return launch_matvec_rows(a, n_wg, st);
+    }
     switch (a.mode) {
     case MV_STORE: return matvec_dispatch<MV_STORE>(a, n_wg, st);
     case MV_ADD: return a.parts ? matvec_dispatch<MV_ADD_MERGED>(a, n_wg, st) : matvec_dispatch<MV_ADD>(a, n_wg, st);

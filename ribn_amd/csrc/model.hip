@@ -887,6 +887,65 @@ hipError_t intdot_rows(ribn_rocm_model* M, const DecodeRows& dr, int n_splits) {
     return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, M->b_argmax, st);
 }
 
+// Float decode rows of a few sequences (up to kMatvecRowsMax): the projections
+// run as the batch-1 matvec launches with several input rows, each weight
+// unit read from HBM once and applied to every row (groups of at most
+// matvec_max_rows(k) rows per launch). Each row's arithmetic is the batch-1
+// step's own, so a row's logits equal those of the same sequence stepped alone.
+constexpr int kMatvecRowsMax = 4;
+
+hipError_t matvec_rows(ribn_rocm_model* M, const DecodeRows& dr, int n_splits) {
+    hipStream_t st = M->stream;
+    const int n = dr.rows;
+    const int qd = M->hq * M->hd, kd = M->hkv * M->hd, ldq = qd + 2 * kd;
+    // one projection over rows [0, n): x rows ldx apart; segment outputs (and
+    // residuals) moved to row r0 at ldo floats per row
+    auto proj = [&](MvArgs a, int n_wg, const float* x, int ldx, const float* norm_w, int ldo, int mode,
+                    std::initializer_list<std::pair<float*, const float*>> outs) {
+        a.norm_w = norm_w;
+        a.mode = mode;
+        a.parts = nullptr;
+        a.ldx = ldx;
+        a.ldo = ldo;
+        const int step = matvec_max_rows(a.k);
+        hipError_t e = hipSuccess;
+        for (int r0 = 0; e == hipSuccess && r0 < n; r0 += step) {
+            MvArgs b = a;
+            b.rows = std::min(step, n - r0);
+            b.x = x + (size_t)r0 * ldx;
+            int i = 0;
+            for (const auto& o : outs) {
+                b.seg[i].out = o.first + (size_t)r0 * ldo;
+                b.seg[i].res = o.second ? o.second + (size_t)r0 * ldo : nullptr;
+                i++;
+            }
+            e = launch_matvec(b, n_wg, st);
+        }
+        return e;
+    };
+    hipError_t e = hipSuccess;
+    for (int l = 0; l < M->L; l++) {
+        const Layer& y = M->layers[l];
+        if ((e = proj(M->mv_qkv[l], M->wg_qkv[l], M->p_h, M->H, y.attn_norm, ldq, MV_STORE,
+                      {{M->p_qkv, nullptr}, {M->p_qkv + qd, nullptr}, {M->p_qkv + qd + kd, nullptr}})) != hipSuccess)
+            return e;
+        AttnArgs at = attn_args(M, l, n_splits);
+        if ((e = launch_attention_rows(at, dr, st)) != hipSuccess) return e;
+        if ((e = proj(M->mv_o[l], M->wg_o[l], M->b_att, qd, nullptr, M->H, MV_ADD, {{M->p_h, M->p_h}})) != hipSuccess)
+            return e;
+        if ((e = proj(M->mv_gu[l], M->wg_gu[l], M->p_h, M->H, y.ffn_norm, M->F, MV_SILU, {{M->b_act, nullptr}})) !=
+            hipSuccess)
+            return e;
+        if ((e = proj(M->mv_down[l], M->wg_down[l], M->b_act, M->F, nullptr, M->H, MV_ADD, {{M->p_h, M->p_h}})) !=
+            hipSuccess)
+            return e;
+    }
+    if ((e = proj(M->mv_head, M->head_wgs, M->p_h, M->H, M->out_norm, M->V, MV_STORE, {{M->b_logits, nullptr}})) !=
+        hipSuccess)
+        return e;
+    return launch_rows_argmax_commit(M->b_logits, M->V, dr, M->d_slots, M->b_argmax, st);
+}
+
 // The projections of batched decode rows run as the chunked-prefill MFMA GEMMs
 // over the rows (or the integer-dot matvec); attention is the split-K decode
 // kernel over each row's own cache; the head is one GEMM over the rows followed
@@ -921,6 +980,7 @@ hipError_t decode_rows_body(ribn_rocm_model* M, int n, int n_splits) {
     if ((e = launch_embed_rows(M->embd, M->d_btokens, n, M->H, M->p_h, st)) != hipSuccess) return e;
     if ((e = launch_rope_rows(M->inv_freq, M->rot, dr, st)) != hipSuccess) return e;
     if (M->int_dot) return intdot_rows(M, dr, n_splits);
+    if (n <= kMatvecRowsMax) return matvec_rows(M, dr, n_splits);
     auto gemm = [&](const uint16_t* x, int k, float* y, int ldy, int mode, std::initializer_list<PrefillSeg> segs,
                     int post = GEMM_POST_NONE, const float* post_w = nullptr, uint16_t* post_out = nullptr,
                     const uint16_t* w16 = nullptr, const float* bias16 = nullptr) {
@@ -1519,10 +1579,8 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
             HIPCHK(dalloc(M, &M->b_counters, sizeof(uint32_t) * R * M->hkv));
             HIPCHK(hipMemsetAsync(M->b_counters, 0, sizeof(uint32_t) * R * M->hkv, M->stream));
             M->h_brows.assign(2 * R, 0);
-            if (M->int_dot) {
-                HIPCHK(dalloc(M, &M->b_xq, sizeof(uint32_t) * R * (kmax / 32) * 9));
-                HIPCHK(dalloc(M, &M->b_act, sizeof(float) * R * M->F));
-            }
+            HIPCHK(dalloc(M, &M->b_act, sizeof(float) * R * M->F));
+            if (M->int_dot) HIPCHK(dalloc(M, &M->b_xq, sizeof(uint32_t) * R * (kmax / 32) * 9));
         }
     }
 

@@ -383,6 +383,28 @@ def test_batched_decode_rows_match_oracle(model_paths, name, gemm):
         _near_tie_match(name, o, ref, ref_logits)
 
 
+@pytest.mark.parametrize("kv", list(KV_MODES))
+@pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen2_q8_0_g7", "qwen3_g8_tied", "qwen3_q4km_hd128_g4"])
+def test_matvec_decode_rows_equal_single_sequences(model_paths, name, kv):
+    """Two to four sequences decoding together run their projections as multi-row matvec launches (each weight
+    read once for every row). A row's arithmetic is the batch-1 step's own, so every sequence's greedy tokens
+    equal those of the same sequence run through the executor alone (same prefill chunks, batch-1 decode
+    steps); the streams also match the FP32 oracle up to near ties."""
+    path = model_paths[name]
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, MODELS[name]["vocab"], n).tolist() for n in (6, 19, 3, 11)]
+    say(f"matvec decode rows {name} kv={kv}")
+    with ribn_amd.QwenRocm(path, context_tokens=64, max_sequences=4, max_batch_tokens=64, kv=kv) as m:
+        alone = [_run_engine(m, [p], 10)[0] for p in prompts]
+        for n in (2, 3, 4):
+            together = _run_engine(m, prompts[:n], 10)
+            assert together == alone[:n], (n, together, alone[:n])
+    kv_round = KV_MODES[kv][0]
+    for p, o in zip(prompts, alone):
+        ref, ref_logits = _oracle_greedy(path, p, 10, 64, kv_round)
+        _near_tie_match(name, o, ref, ref_logits)
+
+
 def test_executor_contract_errors(model_paths):
     path = model_paths["qwen3_q4km_hd64"]
     with ribn_amd.QwenRocm(path, context_tokens=32, max_sequences=1, max_batch_tokens=16) as m:
