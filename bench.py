@@ -293,6 +293,49 @@ def run_config1(args):
     print(json.dumps(out))
 
 
+def run_rows(args):
+    """Decode throughput of N sequences decoding together through the executor ABI (8B shape, Q4_K_M,
+    64-token random prompts, one prefill batch, then 40 decode batches of N rows; median step of the last
+    32, prepare/submit/poll included). 2-4 rows run the multi-row matvec, 5 or more the MFMA GEMMs."""
+    import numpy as np
+    import ribn_amd
+    n = args.rows
+    path = os.path.join("/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir(),
+                        f"ribn_rows_{os.getpid()}.gguf")
+    ribn_amd.synth_qwen_gguf(path, weight_type=ribn_amd.GGML_Q4_K, attn_v_type=ribn_amd.GGML_Q6_K,
+                             ffn_down_type=ribn_amd.GGML_Q6_K, output_type=ribn_amd.GGML_Q6_K,
+                             embd_type=ribn_amd.GGML_Q4_K, **CFG)
+    rng = np.random.default_rng(0)
+    prompts = [rng.integers(0, CFG["vocab"], 64).tolist() for _ in range(n)]
+    try:
+        with ribn_amd.QwenRocm(path, context_tokens=256, max_sequences=max(n, 1), max_batch_tokens=64 * n) as m:
+            for i, p in enumerate(prompts):
+                assert m.admit(i + 1, i + 1, p, 100).kind == ribn_amd.ADMIT_READY
+            def run(batch):
+                m.prepare(batch)
+                sub = m.submit(batch)
+                while m.poll(sub) is None:
+                    pass
+            run([ribn_amd.BatchItem(i + 1, ribn_amd.STEP_PREFILL, 0, 64, 1) for i in range(n)])
+            times = []
+            for step in range(40):
+                t0 = time.perf_counter()
+                run([ribn_amd.BatchItem(i + 1, ribn_amd.STEP_DECODE, 64 + step, 1, 1) for i in range(n)])
+                times.append(time.perf_counter() - t0)
+            for i in range(n):
+                m.release(i + 1)
+    finally:
+        os.unlink(path)
+    t = float(np.median(times[8:]))
+    out = {"metric": f"decode rows: aggregate decode tok/s, {n} sequences decoding together (8B Q4_K_M)",
+           "value": round(n / t, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+           "ms_per_step": round(t * 1e3, 3),
+           "config": {"workload": "8B-shape Q4_K_M batched decode", "sequences": n, "prompt": 64, "steps": 40,
+                      "path": "batch-1 graph step" if n == 1 else
+                      "multi-row matvec" if n <= 4 else "MFMA GEMMs (32-row tiles)"}}
+    print(json.dumps(out))
+
+
 def run_config4(args):
     """32B-shape Q4_K_M, a 32768-token prompt prefilled in 2048-token chunks, then 256 greedy
     tokens; split-K decode attention over the 32K cache dominates beside the 20 GB weight stream."""
@@ -429,6 +472,8 @@ def main():
                     help="configs[3]/[4]: prefill / batched-decode GEMM path (resident = binary16 weight copies)")
     ap.add_argument("--gemv", default="float", choices=["float", "int-dot"],
                     help="configs[3]: decode-row projections (int-dot = the reference's lossy GemvMode::IntegerDot)")
+    ap.add_argument("--rows", type=int, default=0,
+                    help="decode throughput of N sequences decoding together through the executor (its own line)")
     ap.add_argument("--layers", type=int, default=0, help="debug only: fewer layers (invalid as a bench number)")
     ap.add_argument("--probe-traffic", action="store_true",
                     help="counter-collection workload for rocprofv3 --pmc: replays the gate/up, down and head "
@@ -446,6 +491,9 @@ def main():
         return
     if args.q35:
         run_qwen35(args)
+        return
+    if args.rows:
+        run_rows(args)
         return
     if args.config == 1:
         run_config1(args)
