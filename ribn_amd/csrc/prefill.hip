@@ -639,25 +639,30 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
         lrun[t] = 0.f;
     }
 
-    // cache tile in registers: K chunks, and V as key pairs for the transposed store
-    u4v_t kr[KCH], vr[2];
+    // cache tiles in registers (a ring of two: tile t0 + 32 is in flight while
+    // tile t0 is computed): K chunks, and V as key pairs for the transposed store.
+    // Every load is unconditional: a key past the last position re-reads the last
+    // position (written, finite data: its score is masked to -inf and its value
+    // meets a zero probability), so the compiler waits for exactly the tile it
+    // stores, not for the one behind it.
+    struct Tile { u4v_t k[KCH], v[2]; };
+    Tile tb[2];
     auto cache_off = [&](int pos, int c8) {
         const int page = p.pages[pos / kPageTokens];
         return ((size_t)(page * p.hkv + kvh) * kPageTokens + pos % kPageTokens) * HD + c8 * 8;
     };
-    auto load_tile = [&](int t0) {
+    auto load_tile = [&](Tile& tl, int t0) {
 #pragma unroll
         for (int e = 0; e < KCH; e++) {
-            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR, pos = t0 + key;
-            kr[e] = pos <= last_pos ? *reinterpret_cast<const u4v_t*>(p.kcache + cache_off(pos, c8)) : u4v_t{0u, 0u, 0u, 0u};
+            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR, pos = min(t0 + key, last_pos);
+            tl.k[e] = *reinterpret_cast<const u4v_t*>(p.kcache + cache_off(pos, c8));
         }
-        if (tid < VIT) {
-            const int kp = tid / CPR, c8 = tid % CPR;
+        // threads past VIT load a valid row too (unused), so no load is conditional
+        const int kp = (tid % VIT) / CPR, c8 = tid % CPR;
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int pos = t0 + 2 * kp + e;
-                vr[e] = pos <= last_pos ? *reinterpret_cast<const u4v_t*>(p.vcache + cache_off(pos, c8)) : u4v_t{0u, 0u, 0u, 0u};
-            }
+        for (int e = 0; e < 2; e++) {
+            const int pos = min(t0 + 2 * kp + e, last_pos);
+            tl.v[e] = *reinterpret_cast<const u4v_t*>(p.vcache + cache_off(pos, c8));
         }
     };
     // bfloat16 pair (one dword) -> binary16 pair
@@ -666,17 +671,17 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
         const _Float16 a = (_Float16)__uint_as_float(w << 16), b = (_Float16)__uint_as_float(w & 0xffff0000u);
         return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](const Tile& tl) {
 #pragma unroll
         for (int e = 0; e < KCH; e++) {
             const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR;
             *reinterpret_cast<u4v_t*>(&ks[key][c8 * 8]) =
-                u4v_t{to_f16x2(kr[e].x), to_f16x2(kr[e].y), to_f16x2(kr[e].z), to_f16x2(kr[e].w)};
+                u4v_t{to_f16x2(tl.k[e].x), to_f16x2(tl.k[e].y), to_f16x2(tl.k[e].z), to_f16x2(tl.k[e].w)};
         }
         if (tid < VIT) {
             const int kp = tid / CPR, c8 = tid % CPR;
-            const uint32_t a[4] = {to_f16x2(vr[0].x), to_f16x2(vr[0].y), to_f16x2(vr[0].z), to_f16x2(vr[0].w)};
-            const uint32_t b[4] = {to_f16x2(vr[1].x), to_f16x2(vr[1].y), to_f16x2(vr[1].z), to_f16x2(vr[1].w)};
+            const uint32_t a[4] = {to_f16x2(tl.v[0].x), to_f16x2(tl.v[0].y), to_f16x2(tl.v[0].z), to_f16x2(tl.v[0].w)};
+            const uint32_t b[4] = {to_f16x2(tl.v[1].x), to_f16x2(tl.v[1].y), to_f16x2(tl.v[1].z), to_f16x2(tl.v[1].w)};
 #pragma unroll
             for (int d = 0; d < 8; d++) {
                 const uint32_t lo = (a[d / 2] >> (16 * (d & 1))) & 0xffffu, hi = (b[d / 2] >> (16 * (d & 1))) & 0xffffu;
@@ -685,12 +690,10 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
         }
     };
 
-    load_tile(0);
-    for (int t0 = 0; t0 <= last_pos; t0 += kAttKeys) {
-        __syncthreads();   // the previous tile is consumed
-        store_tile();
-        __syncthreads();
-        if (t0 + kAttKeys <= last_pos) load_tile(t0 + kAttKeys);
+    // the tiles past the last one re-read the last tile (their loads stay
+    // unconditional; they are never stored)
+    const int t_last = last_pos / kAttKeys * kAttKeys;
+    auto compute = [&](int t0) {
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
             const int tile = wave + 4 * t, rb = tile / G;
@@ -740,6 +743,22 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
                 acc[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, acc[t][d], 0, 0, 0);
             }
         }
+    };
+    load_tile(tb[0], 0);
+    load_tile(tb[1], min(kAttKeys, t_last));
+    // tile t0 goes from the register ring into LDS, its slot refills with tile
+    // t0 + 64, then tile t0 is computed
+    auto step = [&](Tile& tl, int t0) {
+        __syncthreads();   // the previous tile is consumed
+        store_tile(tl);
+        __syncthreads();
+        load_tile(tl, min(t0 + 2 * kAttKeys, t_last));
+        compute(t0);
+    };
+    for (int t0 = 0; t0 <= last_pos; t0 += 2 * kAttKeys) {
+        step(tb[0], t0);
+        if (t0 + kAttKeys > last_pos) break;
+        step(tb[1], t0 + kAttKeys);
     }
     // acc[t][d][i] = O^T[dim 16 d + 4 j + i][query qn]
 #pragma unroll
