@@ -591,17 +591,19 @@ constexpr int kAttKeys = 32;
 template <int G>
 __host__ __device__ constexpr int att_row_blocks() { return G >= 4 ? 1 : 4 / G; }
 
-template <int HD, int G, bool F16KV>
-__global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
-    constexpr int RB = att_row_blocks<G>();     // 16-row blocks per workgroup
+template <int HD, int G, bool F16KV, int NW>
+__global__ __launch_bounds__(64 * NW) void prefill_attention_kernel(PrefillRows p) {
+    constexpr int NTH = 64 * NW;                // threads
+    constexpr int RB = att_row_blocks<G>() * NW / 4;   // 16-row blocks per workgroup
     constexpr int NT = RB * G;                  // tiles
-    constexpr int TPW = (NT + 3) / 4;           // tiles per wave
+    constexpr int TPW = (NT + NW - 1) / NW;     // tiles per wave
     constexpr int NC = HD / 32;                 // 32-dim chunks of q.k
     constexpr int ND = HD / 16;                 // 16-dim blocks of the output
     constexpr int KLD = HD + 8;                 // K tile row, halves
     constexpr int VLD = kAttKeys + 4;           // V^T row, halves (8-byte aligned rows)
     constexpr int CPR = HD / 8;                 // 16-byte chunks per cache row
-    constexpr int KCH = kAttKeys * CPR / 256;   // K chunks per thread per tile
+    constexpr int KCH = kAttKeys * CPR / NTH;   // K chunks per thread per tile
+    static_assert(KCH >= 1 && KCH * NTH == kAttKeys * CPR, "K tile chunks per thread");
     constexpr int VIT = (kAttKeys / 2) * CPR;   // V (key pair, chunk) items per tile
     __shared__ __attribute__((aligned(16))) _Float16 ks[kAttKeys][KLD];
     __shared__ __attribute__((aligned(16))) _Float16 vts[HD][VLD];
@@ -618,7 +620,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
     float mrun[TPW], lrun[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; t++) {
-        const int tile = wave + 4 * t, rb = tile / G, h = tile % G;
+        const int tile = wave + NW * t, rb = tile / G, h = tile % G;
         const int r = row0 + rb * 16 + qn;
         const bool ok = tile < NT && r < p.m;
         const float* q = p.qout + (size_t)r * ldq + (kvh * G + h) * HD + 8 * j;
@@ -654,7 +656,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
     auto load_tile = [&](Tile& tl, int t0) {
 #pragma unroll
         for (int e = 0; e < KCH; e++) {
-            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR, pos = min(t0 + key, last_pos);
+            const int idx = e * NTH + tid, key = idx / CPR, c8 = idx % CPR, pos = min(t0 + key, last_pos);
             tl.k[e] = *reinterpret_cast<const u4v_t*>(p.kcache + cache_off(pos, c8));
         }
         // threads past VIT load a valid row too (unused), so no load is conditional
@@ -674,7 +676,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
     auto store_tile = [&](const Tile& tl) {
 #pragma unroll
         for (int e = 0; e < KCH; e++) {
-            const int idx = e * 256 + tid, key = idx / CPR, c8 = idx % CPR;
+            const int idx = e * NTH + tid, key = idx / CPR, c8 = idx % CPR;
             *reinterpret_cast<u4v_t*>(&ks[key][c8 * 8]) =
                 u4v_t{to_f16x2(tl.k[e].x), to_f16x2(tl.k[e].y), to_f16x2(tl.k[e].z), to_f16x2(tl.k[e].w)};
         }
@@ -696,7 +698,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
     auto compute = [&](int t0) {
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
-            const int tile = wave + 4 * t, rb = tile / G;
+            const int tile = wave + NW * t, rb = tile / G;
             // wave-uniform: an absent tile, or a row block whose rows all precede the keys
             if (tile >= NT || t0 > p.pos0 + row0 + rb * 16 + 15) continue;
             const int qpos = p.pos0 + row0 + rb * 16 + qn;
@@ -763,7 +765,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillRows p) {
     // acc[t][d][i] = O^T[dim 16 d + 4 j + i][query qn]
 #pragma unroll
     for (int t = 0; t < TPW; t++) {
-        const int tile = wave + 4 * t, rb = tile / G, h = tile % G;
+        const int tile = wave + NW * t, rb = tile / G, h = tile % G;
         const int r = row0 + rb * 16 + qn;
         if (tile >= NT || r >= p.m) continue;
         const float il = 1.0f / lrun[t];
@@ -790,13 +792,29 @@ __global__ void set_pos_kernel(SeqState* s, int pos) {
     if (threadIdx.x == 0) s->pos = pos;
 }
 
+template <int HD, int G, int NW>
+hipError_t attention_launch_prefill_nw(const PrefillRows& p, hipStream_t st) {
+    constexpr int RB = att_row_blocks<G>() * NW / 4;
+    const dim3 grid((p.m + 16 * RB - 1) / (16 * RB), p.hkv);
+    if (p.kv_f16) prefill_attention_kernel<HD, G, true, NW><<<grid, 64 * NW, 0, st>>>(p);
+    else prefill_attention_kernel<HD, G, false, NW><<<grid, 64 * NW, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+// Every workgroup streams the whole key range of its rows' KV head through
+// LDS, so the K/V bytes read per chunk are (key range) x (workgroups per KV
+// head). Over long contexts (a chunk whose last key is past kAttWideKeys)
+// 8-wave workgroups take twice the rows, halving those re-reads (configs[4],
+// 32K context: the launch is bound by them); short prompts keep 4-wave
+// workgroups, which give the GPU more of them.
+constexpr int kAttWideKeys = 4096;
+
 template <int HD, int G>
 hipError_t attention_launch_prefill(const PrefillRows& p, hipStream_t st) {
-    constexpr int RB = att_row_blocks<G>();
-    const dim3 grid((p.m + 16 * RB - 1) / (16 * RB), p.hkv);
-    if (p.kv_f16) prefill_attention_kernel<HD, G, true><<<grid, 256, 0, st>>>(p);
-    else prefill_attention_kernel<HD, G, false><<<grid, 256, 0, st>>>(p);
-    return hipGetLastError();
+    if constexpr (HD == 128) {
+        if (p.pos0 + p.m > kAttWideKeys) return attention_launch_prefill_nw<HD, G, 8>(p, st);
+    }
+    return attention_launch_prefill_nw<HD, G, 4>(p, st);
 }
 
 template <int HD>

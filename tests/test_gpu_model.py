@@ -176,6 +176,28 @@ def test_long_context_split_k(model_paths, kv, step):
 
 
 @pytest.mark.parametrize("kv", list(KV_MODES))
+@pytest.mark.parametrize("g", [4, 8])
+def test_long_prefill_wide_attention(tmp_path, g, kv):
+    """4700 prompt rows in 2048-row chunks with head_dim 128: the last chunk's keys reach past 4096, where the
+    causal chunk attention runs 8-wave workgroups over twice the rows (4-wave before). Logits of rows in every
+    chunk against the FP32 oracle. One layer, so the oracle's quadratic attention stays within seconds."""
+    path = str(tmp_path / f"wide{g}.gguf")
+    ribn_amd.synth_qwen_gguf(path, qwen3=True, hidden=256, layers=1, q_heads=8, kv_heads=8 // g, head_dim=128, ffn=256,
+                             vocab=256, seed=9, norm_jitter=0.15, weight_std=0.05)
+    kv_round, tol = KV_MODES[kv]
+    n = 4700
+    tokens = np.random.default_rng(8).integers(0, 256, n).tolist()
+    say(f"prefill {n} rows g={g} kv={kv}")
+    with ribn_amd.QwenRocm(path, context_tokens=n + 16, max_sequences=1, max_batch_tokens=2048, kv=kv) as m:
+        lg, _ = m.prefill_trace(tokens, chunk=2048, logits=True)
+    ref_l, _ = _oracle_trace(path, tokens, n + 16, kv_round=kv_round)
+    for lo, hi in ((0, 64), (2040, 2100), (4090, 4160), (n - 64, n)):
+        r = _rel(lg[lo:hi], ref_l[lo:hi])
+        say(f"  rows {lo}..{hi}: rel-L2 {r:.2e}")
+        assert r <= tol, (lo, r)
+
+
+@pytest.mark.parametrize("kv", list(KV_MODES))
 def test_split_policy_regimes(tmp_path, kv):
     """8400 positions through every regime of the split policy: one workgroup up to 128 positions, then
     splits of about 128 (up to 2048), 256 (up to 8192) and 1024 positions (flash-decoding blocks across a
