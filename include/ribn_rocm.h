@@ -87,6 +87,11 @@ typedef struct {
  * with RIBN_LOAD_PERSISTENT_STEP or qwen35 hybrids; ribn_rocm_trace and
  * ribn_rocm_prefill_trace refuse such a model. */
 #define RIBN_LOAD_INT_DOT 8u
+/* Let the dequantizing GEMMs (chunked prefill, batched decode rows) read the
+ * weights from the decode planes instead of the default GEMM-ordered copy of
+ * every Q4_K / Q6_K layer matrix and head made at load (one more copy of those
+ * weight bytes in HBM; same values, so the same results). For A/B comparison. */
+#define RIBN_LOAD_GEMM_FROM_PLANES 16u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);

@@ -35,6 +35,7 @@ LOAD_KV_BF16 = 1
 LOAD_PERSISTENT_STEP = 2
 LOAD_RESIDENT_F16 = 4
 LOAD_INT_DOT = 8
+LOAD_GEMM_FROM_PLANES = 16
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -343,13 +344,15 @@ class QwenRocm:
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
                  kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain", gemm: str = "dequant",
-                 gemv: str = "float"):
+                 gemv: str = "float", gemm_copy: bool = True):
         """step: "persistent" (one kernel launch per token step when the library has a kernel compiled for
         this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs).
         gemm: "dequant" (chunked prefill and batched decode on the dequantizing MFMA GEMM) or "resident"
         (binary16 copies of the weights made at load, hipBLASLt GEMMs).
         gemv: "float" (default) or "int-dot": sampled decode rows run the lossy integer-dot projections over
-        Q8_1-packed inputs (the reference's GemvMode::IntegerDot)."""
+        Q8_1-packed inputs (the reference's GemvMode::IntegerDot).
+        gemm_copy: the dequantizing GEMMs read a GEMM-ordered copy of the Q4_K / Q6_K weights made at load
+        (default) or, False, the decode planes (same results; for comparisons)."""
         if gemv not in ("float", "int-dot"):
             raise ValueError("gemv must be 'float' or 'int-dot'")
         if gemm not in ("dequant", "resident"):
@@ -358,7 +361,8 @@ class QwenRocm:
             raise ValueError("step must be 'persistent' or 'chain'")
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
                            (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0)
-                           | (LOAD_RESIDENT_F16 if gemm == "resident" else 0) | (LOAD_INT_DOT if gemv == "int-dot" else 0))
+                           | (LOAD_RESIDENT_F16 if gemm == "resident" else 0) | (LOAD_INT_DOT if gemv == "int-dot" else 0)
+                           | (0 if gemm_copy else LOAD_GEMM_FROM_PLANES))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()

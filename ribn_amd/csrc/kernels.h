@@ -48,7 +48,12 @@ struct QMat {
     const uint8_t* b;
     const uint8_t* c;
     const uint8_t* d;
+    // Q4_K / Q6_K, optional: the GEMM-ordered copy read by the dequantizing GEMM
+    // (one block of kGemmBlkQ4 / kGemmBlkQ6 bytes per 16-row group and 128-wide
+    // K tile, each lane's fragment bytes contiguous; layout in gemm_pack, model.hip)
+    const uint8_t* g;
 };
+constexpr size_t kGemmBlkQ4 = 1216, kGemmBlkQ6 = 1696;
 
 // Per-sequence device state. `pos` is the position of the token the next step
 // consumes (tokens[pos]); the step that samples writes tokens[pos + 1].

@@ -249,6 +249,62 @@ void retile(uint32_t type, const uint8_t* src, uint64_t n_blocks, uint8_t* a, ui
     for (auto& x : th) x.join();
 }
 
+// The GEMM-ordered copy of a Q4_K / Q6_K matrix (QMat::g), from its host
+// planes. Block (n16, kt) holds what the 64 lanes of a wave read for the
+// B fragments of rows 16 n16 .. 16 n16 + 15 (rows past the matrix repeat its
+// last row) and K tile kt (128 values: half a super-block, h = kt % 2), lane =
+// bn + 16 bj reading row 16 n16 + bn:
+//   Q4_K (kGemmBlkQ4 = 1216): [0, 1024) lane's 16 qs bytes (32 (bj/2) + 16 (bj%2)
+//        into the half block), [1024, 1152) scale dword of (bn, bj/2),
+//        [1152, 1216) d|dmin dword of bn;
+//   Q6_K (kGemmBlkQ6 = 1696): [0, 1024) lane's ql bytes 8 bj .. +8 and 32 + 8 bj ..
+//        +8, [1024, 1536) its qh bytes 8 bj .. +8, [1536, 1664) the two 8-bit
+//        sub-block scales of (bn, bj/2) (bytes 0-1: v = 0/2, 2-3: v = 1/3),
+//        [1664, 1696) d of bn.
+// Every read of the GEMM is then one coalesced access per plane of a block.
+size_t gemm_pack_bytes(uint32_t type, uint64_t rows, uint64_t k) {
+    const uint64_t n16 = (rows + 15) / 16, nkt = k / 128;
+    return type == GGML_Q4_K ? n16 * nkt * kGemmBlkQ4 : type == GGML_Q6_K ? n16 * nkt * kGemmBlkQ6 : 0;
+}
+
+void gemm_pack(uint32_t type, uint64_t rows, uint64_t nb, const uint8_t* a, const uint8_t* b, const uint8_t* c,
+               const uint8_t* d, uint8_t* out) {
+    const uint64_t n16c = (rows + 15) / 16, nkt = nb * 2;
+    auto work = [&](uint64_t g0, uint64_t g1) {
+        for (uint64_t n16 = g0; n16 < g1; n16++)
+            for (uint64_t kt = 0; kt < nkt; kt++) {
+                const uint64_t kb = kt >> 1, h = kt & 1;
+                for (int lane = 0; lane < 64; lane++) {
+                    const int bn = lane & 15, bj = lane >> 4;
+                    const uint64_t r = std::min<uint64_t>(n16 * 16 + bn, rows - 1), bi = r * nb + kb;
+                    if (type == GGML_Q4_K) {
+                        uint8_t* o = out + (n16 * nkt + kt) * kGemmBlkQ4;
+                        std::memcpy(o + lane * 16, a + bi * 128 + 64 * h + 32 * (bj >> 1) + 16 * (bj & 1), 16);
+                        if ((bj & 1) == 0) std::memcpy(o + 1024 + (bn * 2 + (bj >> 1)) * 4, b + bi * 16 + 8 * h + 4 * (bj >> 1), 4);
+                        if (bj == 0) std::memcpy(o + 1152 + bn * 4, c + bi * 4, 4);
+                    } else {
+                        uint8_t* o = out + (n16 * nkt + kt) * kGemmBlkQ6;
+                        std::memcpy(o + lane * 16, a + bi * 128 + 64 * h + 8 * bj, 8);
+                        std::memcpy(o + lane * 16 + 8, a + bi * 128 + 64 * h + 32 + 8 * bj, 8);
+                        std::memcpy(o + 1024 + lane * 8, b + bi * 64 + 32 * h + 8 * bj, 8);
+                        if ((bj & 1) == 0) {
+                            const uint8_t* sp = c + bi * 16 + 8 * h + 2 * (bj >> 1);
+                            uint8_t* sd = o + 1536 + (bn * 2 + (bj >> 1)) * 4;
+                            sd[0] = sp[0]; sd[1] = sp[1]; sd[2] = sp[4]; sd[3] = sp[5];
+                        }
+                        if (bj == 0) std::memcpy(o + 1664 + bn * 2, d + bi * 2, 2);
+                    }
+                }
+            }
+    };
+    const int nt = (int)std::min<uint64_t>(16, std::max<uint64_t>(1, n16c / 64));
+    if (nt <= 1) { work(0, n16c); return; }
+    std::vector<std::thread> th;
+    const uint64_t per = (n16c + nt - 1) / nt;
+    for (int t = 0; t < nt; t++) th.emplace_back(work, std::min(n16c, per * t), std::min(n16c, per * (t + 1)));
+    for (auto& x : th) x.join();
+}
+
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 // Plane sizes for a [rows][k] matrix of `type`.
@@ -262,7 +318,7 @@ void plane_sizes(uint32_t type, uint64_t nblocks, size_t* sa, size_t* sb, size_t
 // Allocate planes and upload re-tiled blocks. `blocks` may be host memory of
 // exactly rows*k/block_elems GGUF blocks.
 hipError_t upload_qmat(ribn_rocm_model* M, uint32_t type, uint64_t rows, uint64_t k, const uint8_t* blocks, QMat* out,
-                       std::vector<uint8_t>& staging) {
+                       std::vector<uint8_t>& staging, bool gemm_copy = false) {
     uint64_t be, bb;
     type_layout(type, &be, &bb);
     const uint64_t nblocks = rows * (k / be);
@@ -289,6 +345,16 @@ hipError_t upload_qmat(ribn_rocm_model* M, uint32_t type, uint64_t rows, uint64_
     q.b = dev + (hb - ha);
     q.c = dev + (hc - ha);
     q.d = dev + (hdp - ha);
+    q.g = nullptr;
+    const size_t gbytes = gemm_copy ? gemm_pack_bytes(type, rows, k) : 0;
+    if (gbytes) {
+        std::vector<uint8_t> packed(gbytes);
+        gemm_pack(type, rows, q.nb, ha, hb, hc, hdp, packed.data());
+        uint8_t* gdev = nullptr;
+        if ((e = dalloc(M, &gdev, gbytes)) != hipSuccess) return e;
+        if ((e = hipMemcpy(gdev, packed.data(), gbytes, hipMemcpyHostToDevice)) != hipSuccess) return e;
+        q.g = gdev;
+    }
     *out = q;
     M->weight_bytes += nblocks * bb;
     return hipSuccess;
@@ -1345,6 +1411,8 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     HIPCHK(hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking));
     std::vector<uint8_t> staging;
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
+    // matrices the GEMMs read also get the GEMM-ordered copy (not the embedding table)
+    const bool gemm_copy = !(o.flags & RIBN_LOAD_GEMM_FROM_PLANES);
     auto upload_mat = [&](const GgufTensor* t, uint64_t rows, uint64_t k, QMat* q) -> int {
         if (t->dims.size() != 2 || t->dims[0] != k || t->dims[1] != rows) {
             return fail(nullptr, err, err_len,
@@ -1360,7 +1428,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
                         "tensor " + t->name + ": input length " + std::to_string(k) + " is not a multiple of the " +
                             type_name(t->type) + " block (" + std::to_string(be) + ")",
                         RIBN_ERR_FORMAT);
-        HIPCHK(upload_qmat(M, t->type, rows, k, g.data(*t), q, staging));
+        HIPCHK(upload_qmat(M, t->type, rows, k, g.data(*t), q, staging, gemm_copy && q != &M->embd));
         return RIBN_OK;
     };
     auto upload_f32 = [&](const GgufTensor* t, uint64_t n, float** dst) -> int {

@@ -96,6 +96,15 @@ struct WFrag<12> {
         s = *reinterpret_cast<const uint32_t*>(w.b + (size_t)kb * 16 + 8 * h + o.b);
         qv = *reinterpret_cast<const u4v_t*>(w.a + (size_t)kb * 128 + 64 * h + o.a);
     }
+    // the same bytes from the GEMM-ordered copy: `blk` is the block of this
+    // lane's 16-row group and K tile (QMat::g)
+    __device__ __forceinline__ void fetch_g(const uint8_t* blk) {
+        const int lane = threadIdx.x & 63, bn = lane & 15, bj = lane >> 4;
+        qv = *reinterpret_cast<const u4v_t*>(blk + lane * 16);
+        s = *reinterpret_cast<const uint32_t*>(blk + 1024 + (bn * 2 + (bj >> 1)) * 4);
+        dd = *reinterpret_cast<const uint32_t*>(blk + 1152 + bn * 4);
+    }
+    static constexpr size_t kBlk = kGemmBlkQ4;
     // value = round16(fma(q, sc*d, -m*dmin)): g * q is exact in fp32 (d has
     // 11 significant bits, sc 6, q 4), so the fma rounds once, as the
     // reference's multiply-then-subtract does
@@ -140,6 +149,18 @@ struct WFrag<14> {
         ql1 = *reinterpret_cast<const uint2*>(ap + 32);
         qh = *reinterpret_cast<const uint2*>(w.b + (size_t)kb * 64 + 32 * h + o.b);
     }
+    __device__ __forceinline__ void fetch_g(const uint8_t* blk) {
+        const int lane = threadIdx.x & 63, bn = lane & 15, bj = lane >> 4;
+        const u4v_t q = *reinterpret_cast<const u4v_t*>(blk + lane * 16);
+        ql0 = uint2{q.x, q.y};
+        ql1 = uint2{q.z, q.w};
+        qh = *reinterpret_cast<const uint2*>(blk + 1024 + lane * 8);
+        const uint32_t sc = *reinterpret_cast<const uint32_t*>(blk + 1536 + (bn * 2 + (bj >> 1)) * 4);
+        sc01 = sc & 0xffffu;
+        sc23 = sc >> 16;
+        d16 = *reinterpret_cast<const uint16_t*>(blk + 1664 + bn * 2);
+    }
+    static constexpr size_t kBlk = kGemmBlkQ6;
     // value = round16(round32(d*sc * (q - 32))), q - 32 exact in binary16
     __device__ __forceinline__ h8_t frag(int v) const {
         const float d = canon(d16);
@@ -203,9 +224,11 @@ struct WFrag<8> {
 // B[k = 8(l/16) .. +8][n = l%16]; result C[m = 4(l/16) + i][n = l%16], i < 4.
 // MT (128 or 32) is the workgroup's chunk rows: 32 for batched decode rows,
 // where a 128-row tile would mostly multiply padding.
-template <int T, int MT, bool FULL>
+// GP: the weights come from the GEMM-ordered copy (QMat::g; Q4_K / Q6_K).
+template <int T, int MT, bool FULL, bool GP = false>
 __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg& sg, int m0, int n0, int kt0, int kt1,
                                           int z, uint16_t* xs) {
+    static_assert(!GP || T == 12 || T == 14, "GEMM-ordered copies exist for Q4_K and Q6_K");
     constexpr int MB = MT / 16;                // 16-row blocks of chunk rows
     constexpr int NB = kGemmTileN / 64;        // 16-row weight blocks per wave
     constexpr int XR = MT * 16 / kGemmThreads; // X chunks per thread per K tile
@@ -218,9 +241,17 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) acc[i][nb] = f4_t{0.f, 0.f, 0.f, 0.f};
     typename WFrag<T>::Off woff[NB];
+    const uint8_t* gblk[NB];   // GP: the copy's blocks of this wave's 16-row groups at K tile 0
 #pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-        woff[nb] = WFrag<T>::lane_off(sg.w, (size_t)min(n0 + 16 * NB * wave + 16 * nb + bn, n_rows - 1), bj);
+    for (int nb = 0; nb < NB; nb++) {
+        if constexpr (GP) {
+            // groups past the matrix read its last group (their outputs are not stored)
+            const int n16 = min((n0 >> 4) + NB * wave + nb, (n_rows + 15) / 16 - 1);
+            gblk[nb] = sg.w.g + (size_t)n16 * (sg.w.k / kTileK) * WFrag<T>::kBlk;
+        } else {
+            woff[nb] = WFrag<T>::lane_off(sg.w, (size_t)min(n0 + 16 * NB * wave + 16 * nb + bn, n_rows - 1), bj);
+        }
+    }
     u4v_t xr[XR];
     WFrag<T> w0[NB], w1[NB];   // raw weight bytes of tiles kt and kt + 1
     auto fetch_x = [&](int kt) {
@@ -249,7 +280,8 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
     auto fetch_w = [&](WFrag<T> (&wf)[NB], int kt) {
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) {
-            if constexpr (FULL && T == 8) wf[nb].fetch_full(sg.w, woff[nb], kt);
+            if constexpr (GP) wf[nb].fetch_g(gblk[nb] + (size_t)kt * WFrag<T>::kBlk);
+            else if constexpr (FULL && T == 8) wf[nb].fetch_full(sg.w, woff[nb], kt);
             else wf[nb].fetch(sg.w, woff[nb], kt);
         }
     };
@@ -325,7 +357,7 @@ __device__ __forceinline__ void gemm_tile(const PrefillGemm& g, const PrefillSeg
     }
 }
 
-template <int TA, int TB, int MT>
+template <int TA, int TB, int MT, bool GP = false>
 __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm g) {
     extern __shared__ __attribute__((aligned(16))) uint16_t plds[];   // X tiles [2][MT][kLdsRow]
     int si = 0;
@@ -340,15 +372,15 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
     // rows: configs[3] decode phase 4.24k -> 4.47k tok/s) and cost at 128-row
     // tiles (512-token prefill 27.2k -> 23.4k tok/s), so only the former use them.
     if (MT != 32 || g.k % kTileK) {   // uniform: a partial last K tile needs the conditional fetches
-        if (si == 2 && TB != TA) gemm_tile<TB, MT, false>(g, sg, m0, n0, kt0, kt1, z, plds);
-        else gemm_tile<TA, MT, false>(g, sg, m0, n0, kt0, kt1, z, plds);
+        if (si == 2 && TB != TA) gemm_tile<TB, MT, false, GP>(g, sg, m0, n0, kt0, kt1, z, plds);
+        else gemm_tile<TA, MT, false, GP>(g, sg, m0, n0, kt0, kt1, z, plds);
         return;
     }
     if constexpr (TA == TB) {
-        gemm_tile<TA, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
+        gemm_tile<TA, MT, true, GP>(g, sg, m0, n0, kt0, kt1, z, plds);
     } else {
-        if (si == 2) gemm_tile<TB, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
-        else gemm_tile<TA, MT, true>(g, sg, m0, n0, kt0, kt1, z, plds);
+        if (si == 2) gemm_tile<TB, MT, true, GP>(g, sg, m0, n0, kt0, kt1, z, plds);
+        else gemm_tile<TA, MT, true, GP>(g, sg, m0, n0, kt0, kt1, z, plds);
     }
 }
 
@@ -907,27 +939,39 @@ hipError_t launch_prefill_gemm(const PrefillGemm& g, hipStream_t st) {
     PrefillGemm gg = g;
     gg.ksplit = ks;
     const size_t lds = (size_t)2 * mt * kLdsRow * 2;
-#define RIBN_PG(A, B)                                                                                           \
-    if (ta == A && tb == B) {                                                                                   \
+    // the GEMM-ordered copies (QMat::g) when every segment has one
+    bool gp = true;
+    for (int i = 0; i < g.nseg; i++) gp = gp && g.seg[i].w.g != nullptr && (g.seg[i].w.type == 12 || g.seg[i].w.type == 14);
+#define RIBN_PG_LAUNCH(A, B, P)                                                                                 \
+    {                                                                                                           \
         hipError_t e;                                                                                           \
         if (mt == 32) {                                                                                         \
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, 32>),              \
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, 32, P>),           \
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
             if (e != hipSuccess) return e;                                                                      \
-            prefill_gemm_kernel<A, B, 32><<<grid, kGemmThreads, lds, st>>>(gg);                                 \
+            prefill_gemm_kernel<A, B, 32, P><<<grid, kGemmThreads, lds, st>>>(gg);                              \
         } else {                                                                                                \
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, kTileM>),          \
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_gemm_kernel<A, B, kTileM, P>),       \
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                      \
             if (e != hipSuccess) return e;                                                                      \
-            prefill_gemm_kernel<A, B, kTileM><<<grid, kGemmThreads, lds, st>>>(gg);                             \
+            prefill_gemm_kernel<A, B, kTileM, P><<<grid, kGemmThreads, lds, st>>>(gg);                          \
         }                                                                                                       \
         e = hipGetLastError();                                                                                  \
         if (e != hipSuccess) return e;                                                                          \
         return gemm_post(g, ks, st);                                                                            \
     }
-    RIBN_PG(12, 12) RIBN_PG(14, 14) RIBN_PG(8, 8) RIBN_PG(12, 14) RIBN_PG(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
+#define RIBN_PG(A, B) \
+    if (ta == A && tb == B) RIBN_PG_LAUNCH(A, B, false)
+#define RIBN_PG2(A, B)                           \
+    if (ta == A && tb == B) {                    \
+        if (gp) RIBN_PG_LAUNCH(A, B, true)       \
+        RIBN_PG_LAUNCH(A, B, false)              \
+    }
+    RIBN_PG2(12, 12) RIBN_PG2(14, 14) RIBN_PG(8, 8) RIBN_PG2(12, 14) RIBN_PG2(14, 12) RIBN_PG(12, 8) RIBN_PG(8, 12)
     RIBN_PG(14, 8) RIBN_PG(8, 14)
 #undef RIBN_PG
+#undef RIBN_PG2
+#undef RIBN_PG_LAUNCH
     return hipErrorInvalidValue;
 }
 

@@ -175,6 +175,27 @@ def test_long_context_split_k(model_paths, kv, step):
         assert r <= tol, (lo, r)
 
 
+@pytest.mark.parametrize("name", ["qwen3_q4km_hd64", "qwen3_q4km_hd128_g4", "qwen3_g8_tied"])
+def test_gemm_copy_matches_planes(model_paths, name):
+    """The dequantizing GEMMs read the GEMM-ordered copy of the Q4_K / Q6_K weights by default, the decode
+    planes with gemm_copy=False: the same bytes into the same arithmetic, so chunked-prefill logits and hidden
+    states and batched decode rows (five sequences, MFMA GEMMs with 32-row tiles) are bit-identical."""
+    path = model_paths[name]
+    rng = np.random.default_rng(13)
+    tokens = rng.integers(0, MODELS[name]["vocab"], 200).tolist()
+    prompts = [rng.integers(0, MODELS[name]["vocab"], n).tolist() for n in (5, 17, 9, 33, 2)]
+    out = {}
+    for copy in (True, False):
+        say(f"gemm copy={copy} {name}")
+        with ribn_amd.QwenRocm(path, context_tokens=256, max_sequences=5, max_batch_tokens=128, gemm_copy=copy) as m:
+            lg, hd = m.prefill_trace(tokens, chunk=128, logits=True, hidden=True)
+            rows = _run_engine(m, prompts, 8)
+        out[copy] = (lg, hd, rows)
+    assert np.array_equal(out[True][0], out[False][0])
+    assert np.array_equal(out[True][1], out[False][1])
+    assert out[True][2] == out[False][2]
+
+
 @pytest.mark.parametrize("kv", list(KV_MODES))
 @pytest.mark.parametrize("g", [4, 8])
 def test_long_prefill_wide_attention(tmp_path, g, kv):
