@@ -389,6 +389,15 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(PrefillGemm 
 // reduction waits for ks / 4 L2 round trips instead of ks.
 __device__ __forceinline__ float4 add_splits(float4 a, const float* part, size_t stride, size_t i, int ks) {
     int z = 0;
+    for (; z + 8 <= ks; z += 8) {
+        float4 p[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) p[q] = *reinterpret_cast<const float4*>(part + (size_t)(z + q) * stride + i);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            a.x += p[q].x; a.y += p[q].y; a.z += p[q].z; a.w += p[q].w;
+        }
+    }
     for (; z + 4 <= ks; z += 4) {
         float4 p[4];
 #pragma unroll
@@ -426,15 +435,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_rms_kernel(const float* par
     const size_t plane = (size_t)m * n, row = (size_t)r * n;
     float4 v[8];
     float ss = 0.f;
+    // every sum first (no store in between, so the loads of all of a thread's
+    // groups and splits can be in flight together), then the stores
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = 4 * tid + 1024 * j;
+        if (i < n)
+            v[j] = add_splits(res ? *reinterpret_cast<const float4*>(res + row + i) : float4{0.f, 0.f, 0.f, 0.f}, part,
+                              plane, row + i, ks);
+    }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const int i = 4 * tid + 1024 * j;
         if (i < n) {
-            const float4 a = add_splits(res ? *reinterpret_cast<const float4*>(res + row + i) : float4{0.f, 0.f, 0.f, 0.f},
-                                        part, plane, row + i, ks);
+            const float4 a = v[j];
             *reinterpret_cast<float4*>(y + row + i) = a;
             ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
-            v[j] = a;
         }
     }
     ss = wave_sum(ss);
