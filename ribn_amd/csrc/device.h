@@ -650,11 +650,13 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     constexpr int MODE = MERGE ? MV_ADD : MODE_;
     const int total = w.n_items * w.ngr;
     constexpr bool EARLY = std::remove_reference_t<Sync>::kEarlyX && !MERGE;
-    // the residual launches (O, down) take a long input without norm: four passes
-    // early (k up to 32768 at 512 threads). Their norm weights are a compile-time
-    // null, so no staging pass holds a conditional load, whose wait would cover the
-    // weight loads in flight as well.
-    constexpr int NP = EARLY ? (MODE == MV_ADD ? 4 : 1) : 0;
+    // the residual launches (O, down) take a long input without norm: two passes
+    // early (k up to 16384 at 512 threads; the rest is loaded while staging). Their
+    // norm weights are a compile-time null, so no staging pass holds a conditional
+    // load, whose wait would cover the weight loads in flight as well. Four early
+    // passes measured slower on the 8B down launch (11.6 us against 10.7 us with
+    // the 2-deep Q6_K ring): the extra loads delay the weight stream behind them.
+    constexpr int NP = EARLY ? (MODE == MV_ADD ? 2 : 1) : 0;
     const float* const norm_w = MODE == MV_ADD ? nullptr : a.norm_w;
     XPre<NP == 0 ? 1 : NP> pre;
     if constexpr (NP > 0) stage_pre<NP>(a.x, norm_w, a.k, pre);

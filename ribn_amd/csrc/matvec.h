@@ -8,12 +8,13 @@ namespace {
 
 // Ring depth (load groups in flight per wave) of the standalone matvec, per type.
 // Under the one-workgroup-per-CU layout, the Q4_K gate/up launch measured 12.7 us
-// at depth 2, 13.3 us at depth 3 and 16.0 us at depth 6.
+// at depth 2, 13.3 us at depth 3 and 16.0 us at depth 6; the Q6_K down launch
+// 10.7 us at depth 2 against 11.7 us at depth 3 (two early input passes).
 #ifndef RIBN_RING_SA_Q4
 #define RIBN_RING_SA_Q4 2
 #endif
 #ifndef RIBN_RING_SA_Q6
-#define RIBN_RING_SA_Q6 3
+#define RIBN_RING_SA_Q6 2
 #endif
 #ifndef RIBN_RING_SA_Q8
 #define RIBN_RING_SA_Q8 3
