@@ -667,8 +667,14 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     for (int r = 0; r < R; r++) addend[r] = (MODE == MV_ADD || sg.bias) ? mv_addend(sg, w, MODE, (size_t)r * a.ldo) : 0.f;
     Group<T> ring[D];
     Cursor ld{0, 0};
+    // A standalone launch issues one group before staging and the rest after it:
+    // every workgroup's first loads go out together, and the fewer there are, the
+    // sooner the address unit reaches the staging code (8B decode: 593 -> 598-603
+    // tok/s against the whole ring first). The persistent step issues the whole
+    // ring before its grid barrier, whose wait it overlaps.
+    constexpr int DP = std::remove_reference_t<Sync>::kEarlyX ? 1 : D;
 #pragma unroll
-    for (int j = 0; j < D; j++) {
+    for (int j = 0; j < DP; j++) {
         load_group<T>(ring[j], w, ld.it, ld.gi);
         ld.next(w.ngr);
     }
@@ -688,6 +694,11 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
                                    reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(gs) + r * rb), red);
     }
     sync.mark();
+#pragma unroll
+    for (int j = DP; j < D; j++) {
+        load_group<T>(ring[j], w, ld.it, ld.gi);
+        ld.next(w.ngr);
+    }
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
     float a0[R], b0[R];
 #pragma unroll
