@@ -575,6 +575,32 @@ __device__ __forceinline__ void mv_group(const Group<T>& g, const WaveWork& w, c
     }
 }
 
+// Rows of 129-160 units (k = 4352 ... 5120 for Q4_K / Q6_K, e.g. the 32B
+// shape's hidden 5120) take two load groups per item, the second holding at
+// most 32 units of each row. That tail group runs with one unit per lane:
+// lanes 0-31 take row a's tail units, lanes 32-63 row b's, in slot a0 only,
+// so it costs a quarter of a full group's loads and arithmetic.
+template <int T>
+__device__ __forceinline__ void load_tail(Group<T>& g, const WaveWork& w, int it) {
+    using U = Unit<T>;
+    const int item = w.first_item + it * w.stride;
+    const int ra = w.pair ? item : 2 * item;
+    const int rb = w.pair ? item : min(ra + 1, w.n_rows - 1);
+    const int lane = threadIdx.x & 63, hi = lane >> 5;
+    const int l = 128 + (lane & 31) < w.n_units ? (lane & 31) : 0;
+    g.a0 = U::load_full(hi ? w.wb : w.wa, (size_t)(hi ? rb : ra), 128, l);
+}
+template <int T, int R>
+__device__ __forceinline__ void mv_tail(const Group<T>& g, const WaveWork& w, const u4_t* xs4, const float* gs,
+                                        float (&a0)[R], float (&b0)[R]) {
+    static_assert(R == 1, "tail groups run for one input row");
+    using U = Unit<T>;
+    const int lane = threadIdx.x & 63, u = 128 + (lane & 31);
+    const float t = u < w.n_units ? U::apply(g.a0, u, xs4, w.n_units, gs, 0.f) : 0.f;
+    if (lane < 32) a0[0] += t;
+    else b0[0] += t;
+}
+
 // The input of an attention-output projection whose attention launch left its
 // split partials unmerged (AttnArgs::defer):
 //   x[h HD + d] = sum_s w_s o_s[h][d] / sum_s w_s l_s,  w_s = 2^(m_s - max_s m_s)
@@ -642,9 +668,12 @@ __device__ __forceinline__ float stage_merged(const MvArgs& a, MergePre& mp, int
 // R > 1: R input rows (MvArgs::rows, ldx floats apart) staged rb bytes apart in
 // LDS, outputs (and residuals) ldo floats apart; each weight unit is loaded
 // once and applied to every row.
-template <int T, int MODE_, int D, int R, typename Sync>
+// TAIL: every item is one full group and one tail group (two groups a row,
+// D = 2), so ring slot 0 always holds full groups and slot 1 tail groups.
+template <int T, int MODE_, int D, int R, typename Sync, bool TAIL = false>
 __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const WaveWork& w, int8_t* xs, float* gs,
                                         float* red, size_t rb, uint64_t& best, Sync&& sync) {
+    static_assert(!TAIL || (D == 2 && R == 1), "tail groups alternate with full ones in a 2-deep ring");
     constexpr bool MERGE = MODE_ == MV_ADD_MERGED;
     static_assert(R == 1 || !MERGE, "merged attention partials take one row");
     constexpr int MODE = MERGE ? MV_ADD : MODE_;
@@ -675,7 +704,8 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     constexpr int DP = std::remove_reference_t<Sync>::kEarlyX ? 1 : D;
 #pragma unroll
     for (int j = 0; j < DP; j++) {
-        load_group<T>(ring[j], w, ld.it, ld.gi);
+        if (TAIL && (j & 1)) load_tail<T>(ring[j], w, ld.it);
+        else load_group<T>(ring[j], w, ld.it, ld.gi);
         ld.next(w.ngr);
     }
     int ldq = D;   // index of the group `ld` points at
@@ -696,7 +726,8 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     sync.mark();
 #pragma unroll
     for (int j = DP; j < D; j++) {
-        load_group<T>(ring[j], w, ld.it, ld.gi);
+        if (TAIL && (j & 1)) load_tail<T>(ring[j], w, ld.it);
+        else load_group<T>(ring[j], w, ld.it, ld.gi);
         ld.next(w.ngr);
     }
     const u4_t* xs4 = reinterpret_cast<const u4_t*>(xs);
@@ -708,8 +739,13 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
     for (; q0 + D < total; q0 += D) {
 #pragma unroll
         for (int j = 0; j < D; j++) {
-            mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
-            load_group<T>(ring[j], w, ld.it, ld.gi);
+            if (TAIL && (j & 1)) {
+                if constexpr (TAIL) mv_tail<T, R>(ring[j], w, xs4, gs, a0, b0);
+                load_tail<T>(ring[j], w, ld.it);
+            } else {
+                mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
+                load_group<T>(ring[j], w, ld.it, ld.gi);
+            }
             if (ldq + 1 < total) {
                 ld.next(w.ngr);
                 ++ldq;
@@ -721,7 +757,11 @@ __device__ __forceinline__ bool mv_ring(const MvArgs& a, const MvSeg& sg, const 
 #pragma unroll
     for (int j = 0; j < D; j++) {
         if (q0 + j < total) {
-            mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
+            if (TAIL && (j & 1)) {
+                if constexpr (TAIL) mv_tail<T, R>(ring[j], w, xs4, gs, a0, b0);
+            } else {
+                mv_group<T, R>(ring[j], w, c, xs4, gs, rb, a0, b0);
+            }
             mv_finish<T, MODE, R>(sg, w, c, a0, b0, oscale, addend, best, (size_t)a.ldo);
             c.next(w.ngr);
         }
@@ -742,6 +782,10 @@ __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWor
     // depth: one that divides the wave's group count (no refill past the end),
     // or the full depth when the count is large enough for a few reloads of the
     // last group not to matter
+    if constexpr (R == 1 && P >= 2 && std::remove_reference_t<Sync>::kEarlyX && T != 8) {
+        if (w.ngr == 2 && w.n_units - 128 <= 32)
+            return mv_ring<T, MODE, 2, R, std::remove_reference_t<Sync>&, true>(a, sg, w, xs, gs, red, rb, best, sync);
+    }
     if (total >= P && (total % P == 0 || total >= 3 * P)) return mv_ring<T, MODE, P, R>(a, sg, w, xs, gs, red, rb, best, sync);
     if constexpr (P > 3) {
         if (total >= 3 && total % 3 == 0) return mv_ring<T, MODE, 3, R>(a, sg, w, xs, gs, red, rb, best, sync);

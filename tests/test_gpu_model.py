@@ -37,6 +37,10 @@ MODELS = {
                                   ffn=4864, vocab=1024, weight_type=ribn_amd.GGML_Q8_0),
     "qwen3_g8_tied": dict(qwen3=True, hidden=512, layers=1, q_heads=8, kv_heads=1, head_dim=64, ffn=512,
                           vocab=256, tied_output=True, **Q4KM),
+    # rows of 136 (hidden 4352) and 144 (FFN 4608) units: q|k|v, gate/up and down run a full load group
+    # and a tail group per item, like the 32B shape's hidden 5120
+    "qwen3_q4km_row_tail": dict(qwen3=True, hidden=4352, layers=1, q_heads=8, kv_heads=2, head_dim=128, ffn=4608,
+                                vocab=256, **Q4KM),
 }
 
 
