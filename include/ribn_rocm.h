@@ -92,6 +92,11 @@ typedef struct {
  * every Q4_K / Q6_K layer matrix and head made at load (one more copy of those
  * weight bytes in HBM; same values, so the same results). For A/B comparison. */
 #define RIBN_LOAD_GEMM_FROM_PLANES 16u
+/* Merge a long context's decode-attention split partials (more than 8 splits)
+ * inside the attention launch, one workgroup per KV head, instead of in the
+ * separate merge launch the chain uses by default. Same log-sum-exp merge, so
+ * the same results up to summation order. For A/B comparison. */
+#define RIBN_LOAD_ATTN_MERGE_IN_LAUNCH 32u
 
 int ribn_rocm_load_gguf(const char *path, const ribn_rocm_load_options *opts, ribn_rocm_model **out,
                         char *err, size_t err_len);

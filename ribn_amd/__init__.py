@@ -36,6 +36,7 @@ LOAD_PERSISTENT_STEP = 2
 LOAD_RESIDENT_F16 = 4
 LOAD_INT_DOT = 8
 LOAD_GEMM_FROM_PLANES = 16
+LOAD_ATTN_MERGE_IN_LAUNCH = 32
 ADMIT_READY, ADMIT_REJECTED, ADMIT_DEFERRED = 0, 1, 2
 STEP_PREFILL, STEP_DECODE = 0, 1
 
@@ -344,7 +345,7 @@ class QwenRocm:
 
     def __init__(self, path: str, *, context_tokens: int = 0, max_sequences: int = 0, max_batch_tokens: int = 0,
                  kv_pages: int = 0, device: int = 0, kv: str = "f16", step: str = "chain", gemm: str = "dequant",
-                 gemv: str = "float", gemm_copy: bool = True):
+                 gemv: str = "float", gemm_copy: bool = True, attn_merge: str = "apart"):
         """step: "persistent" (one kernel launch per token step when the library has a kernel compiled for
         this model's configuration, else the launch chain) or "chain" (per-stage launches in HIP graphs).
         gemm: "dequant" (chunked prefill and batched decode on the dequantizing MFMA GEMM) or "resident"
@@ -352,7 +353,11 @@ class QwenRocm:
         gemv: "float" (default) or "int-dot": sampled decode rows run the lossy integer-dot projections over
         Q8_1-packed inputs (the reference's GemvMode::IntegerDot).
         gemm_copy: the dequantizing GEMMs read a GEMM-ordered copy of the Q4_K / Q6_K weights made at load
-        (default) or, False, the decode planes (same results; for comparisons)."""
+        (default) or, False, the decode planes (same results; for comparisons).
+        attn_merge: "apart" (default: a long context's decode-attention split partials are merged by a launch
+        of their own) or "in-launch" (the attention launch merges them; for comparisons)."""
+        if attn_merge not in ("apart", "in-launch"):
+            raise ValueError("attn_merge must be 'apart' or 'in-launch'")
         if gemv not in ("float", "int-dot"):
             raise ValueError("gemv must be 'float' or 'int-dot'")
         if gemm not in ("dequant", "resident"):
@@ -362,7 +367,8 @@ class QwenRocm:
         opts = LoadOptions(context_tokens, max_sequences, max_batch_tokens, kv_pages, device,
                            (LOAD_KV_BF16 if kv == "bf16" else 0) | (LOAD_PERSISTENT_STEP if step == "persistent" else 0)
                            | (LOAD_RESIDENT_F16 if gemm == "resident" else 0) | (LOAD_INT_DOT if gemv == "int-dot" else 0)
-                           | (0 if gemm_copy else LOAD_GEMM_FROM_PLANES))
+                           | (0 if gemm_copy else LOAD_GEMM_FROM_PLANES)
+                           | (LOAD_ATTN_MERGE_IN_LAUNCH if attn_merge == "in-launch" else 0))
         if kv not in ("f16", "bf16"):
             raise ValueError("kv must be 'f16' or 'bf16'")
         h = ctypes.c_void_p()

@@ -1134,18 +1134,26 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     //                               accumulators: lane group bj's logical k
     //                               0..7 are positions 4bj..4bj+3, 16+4bj..+3
     //    The S^T / O^T orientation keeps each head in lane % 16. A bfloat16
-    //    cache is converted to binary16 (exact in binary16's normal range).
+    //    cache feeds v_mfma_f32_16x16x32_bf16 as stored; q and P then enter as
+    //    two bfloat16 terms each (x = hi + lo, hi = bf16(x), lo = bf16(x - hi):
+    //    16 significant bits, finer than binary16), two MFMAs per product.
     //    The current position's k and v come from LDS, not the cache.
     {
         typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
+        typedef __bf16 b8v_t __attribute__((ext_vector_type(8)));
         typedef float f4v_t __attribute__((ext_vector_type(4)));
         constexpr int NDB = HD / 16;   // 16-dim blocks of the output
-        auto to_f16x2 = [](uint32_t w) -> uint32_t {
-            if constexpr (F16) return w;
-            const _Float16 x = (_Float16)__uint_as_float(w << 16), y = (_Float16)__uint_as_float(w & 0xffff0000u);
-            return (uint32_t)__builtin_bit_cast(uint16_t, x) | ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+        // x as bfloat16 hi + lo terms (8 values)
+        auto split_bf16 = [](const float (&x)[8], b8v_t& hi, b8v_t& lo) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const __bf16 h = (__bf16)x[e];
+                hi[e] = h;
+                lo[e] = (__bf16)(x[e] - (float)h);
+            }
         };
         h8v_t qb[KC];
+        b8v_t qbh[KC], qbl[KC];
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const int d = bj * (HD / 4) + 8 * c;
@@ -1154,8 +1162,13 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 lo = *reinterpret_cast<const float4*>(&buf[bn][d]);
                 hi = *reinterpret_cast<const float4*>(&buf[bn][d + 4]);
             }
-            qb[c] = h8v_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
-                          (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+            if constexpr (F16) {
+                qb[c] = h8v_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+                              (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+            } else {
+                const float q8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                split_bf16(q8, qbh[c], qbl[c]);
+            }
         }
         const int own = owner ? pos - t0 : -1;   // the current position within the split
         uint32_t* vt = reinterpret_cast<uint32_t*>(&L.vts[wave][0][0]);   // [HD][kVtLd / 2] position pairs
@@ -1168,7 +1181,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 const u4_t y = tl + 1 == own ? *reinterpret_cast<const u4_t*>(&L.vq[c8 * 8]) : v[it][1];
 #pragma unroll
                 for (int w = 0; w < 4; w++) {
-                    const uint32_t xw = to_f16x2(dword_at(x, w)), yw = to_f16x2(dword_at(y, w));
+                    const uint32_t xw = dword_at(x, w), yw = dword_at(y, w);   // cache precision, as stored
                     vt[(c8 * 8 + 2 * w) * (kVtLd / 2) + pp] = (xw & 0xffffu) | (yw << 16);
                     vt[(c8 * 8 + 2 * w + 1) * (kVtLd / 2) + pp] = (xw >> 16) | (yw & 0xffff0000u);
                 }
@@ -1196,8 +1209,13 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 st[h] = f4v_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < KC; c++) {
-                    const u4_t kb{to_f16x2(kr[h][c].x), to_f16x2(kr[h][c].y), to_f16x2(kr[h][c].z), to_f16x2(kr[h][c].w)};
-                    st[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, kb), qb[c], st[h], 0, 0, 0);
+                    if constexpr (F16) {
+                        st[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, kr[h][c]), qb[c], st[h], 0, 0, 0);
+                    } else {
+                        const b8v_t kb = __builtin_bit_cast(b8v_t, kr[h][c]);
+                        st[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qbh[c], st[h], 0, 0, 0);
+                        st[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qbl[c], st[h], 0, 0, 0);
+                    }
                 }
             }
             // positions b0 + 16h + 4bj + i; those past the split are masked
@@ -1222,8 +1240,14 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
 #pragma unroll
             for (int e = 0; e < 8; e++) lsum += ps[e];
             l_run = l_run * alpha + lsum;
-            const h8v_t pb{(_Float16)ps[0], (_Float16)ps[1], (_Float16)ps[2], (_Float16)ps[3],
+            h8v_t pb;
+            b8v_t pbh, pbl;
+            if constexpr (F16) {
+                pb = h8v_t{(_Float16)ps[0], (_Float16)ps[1], (_Float16)ps[2], (_Float16)ps[3],
                            (_Float16)ps[4], (_Float16)ps[5], (_Float16)ps[6], (_Float16)ps[7]};
+            } else {
+                split_bf16(ps, pbh, pbl);
+            }
             const uint16_t* vrow = &L.vts[wave][0][0];
 #pragma unroll
             for (int db = 0; db < NDB; db++) {
@@ -1232,7 +1256,12 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
                 const uint2 hi = *reinterpret_cast<const uint2*>(r + 16 + 4 * bj);
                 const u4_t va{lo.x, lo.y, hi.x, hi.y};
                 acc[db] *= alpha;
-                acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, va), pb, acc[db], 0, 0, 0);
+                if constexpr (F16) {
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8v_t, va), pb, acc[db], 0, 0, 0);
+                } else {
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8v_t, va), pbh, acc[db], 0, 0, 0);
+                    acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8v_t, va), pbl, acc[db], 0, 0, 0);
+                }
             }
         };
         // Blocks with a successor in this wave prefetch it; the wave's last block
@@ -1283,7 +1312,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
     sync.phase(6);
     const bool direct = a.n_splits == 1;
     float* rec = a.part + ((size_t)kvh * a.n_splits + split) * REC;
-    if (a.defer && !direct) {
+    if (a.defer == 1 && !direct) {
         // records left for merge_parts hold the unnormalized output in binary16
         // (pairs of values per word in the record's first G*HD/2 words): half the
         // bytes for every workgroup of the projection that reads them all
@@ -1314,7 +1343,7 @@ __device__ bool attention_item(const AttnArgs& a, int split, int kvh, int pos, c
         st_agent(rec + G * HD + tid, n > 0 ? stat[0][tid] : -INFINITY);
         st_agent(rec + G * HD + G + tid, n > 0 ? stat[1][tid] : 0.f);
     }
-    if (a.defer) return true;   // the next launch merges the records (merge_parts)
+    if (a.defer) return true;   // a later launch merges the records (merge_parts, attention_merge_kernel)
     sync.phase(7);
     if (!arrive_last(a.counters + kvh, a.n_splits)) return true;
     sync.phase(8);

@@ -13,14 +13,17 @@ constexpr int kMaxSplitTokens = 2048;   // positions one attention workgroup cov
 // Decode-attention splits for a context of `ctx` positions, a power of two
 // (measured on MI355X for head_dim 64 and 128, 1 to 8 query heads per KV head):
 // one workgroup up to 128 positions; at least 4 and about 128 positions each up
-// to 2048; about 256 each up to 8192 and about 1024 beyond, at most kMaxSplits
+// to 2048; about 256 each up to 8192 and beyond that at least 32 splits of at
+// most about 1024 positions, at most kMaxSplits
 // (a split then covers at most kMaxSplitTokens positions for contexts up to
 // kMaxSplits * kMaxSplitTokens).
 __host__ __device__ inline int splits_for_ctx(int ctx) {
     if (ctx <= 128) return 1;
     const int per = ctx <= 2048 ? 128 : ctx <= 8192 ? 256 : 1024;
     const int want = (ctx + per - 1) / per;
-    int s = 4;
+    // beyond 8192 positions at least 32 splits (16K: 18.8 us against 25.6 us at
+    // 16 splits for the 32B shape with the separate merge launch)
+    int s = ctx <= 8192 ? 4 : 32;
     while (s < want && s < kMaxSplits) s <<= 1;
     return s;
 }
@@ -131,6 +134,8 @@ constexpr int kMvMaxRows = 4;
 // Largest split count whose partials the attention-output projection merges
 // itself (AttnArgs::defer); beyond it the attention launch merges them.
 constexpr int kDeferMaxSplits = 8;
+// Largest split count the separate merge launch takes (one split per lane).
+constexpr int kMergeMaxSplits = 64;
 
 // Per-step rotary table: cos/sin of theta_p = pos * base^(-2p/rot) for the
 // active sequence's position, written by the embedding kernel.
@@ -156,8 +161,10 @@ struct AttnArgs {
     float* out;              // [hq][hd]
     const StepCtl* ctl;
     int32_t hq, hkv, hd, rot, n_splits, kv_f16;
-    int32_t defer;           // 1 < n_splits <= kDeferMaxSplits: leave the split partials in `part`
-                             // for the next matvec (MvArgs::parts) instead of merging them here
+    int32_t defer;           // 1 (1 < n_splits <= kDeferMaxSplits): leave the split partials in `part`, the
+                             // output in binary16, for the next matvec (MvArgs::parts) to merge;
+                             // 2 (kDeferMaxSplits < n_splits <= kMergeMaxSplits): leave them (fp32) for
+                             // attention_merge_kernel; 0: the attention launch merges them itself
     float eps;
     float scale_log2;        // log2(e) / sqrt(hd)
 };
@@ -291,6 +298,7 @@ size_t matvec_lds_bytes(int k, int rows = 1);
 // must fit the 160 KB of LDS), at most kMvMaxRows.
 int matvec_max_rows(int k);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+hipError_t launch_attention_merge(const AttnArgs& a, hipStream_t stream);
 
 // Batched decode: one decode row per sequence, all in one step. Row r consumes
 // the token at position pos[r] of the sequence in slot slot[r]; its page table

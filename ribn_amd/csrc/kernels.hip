@@ -260,10 +260,68 @@ hipError_t launch_matvec(const MvArgs& a, int n_wg, hipStream_t st) {
     }
 }
 
+// Merge of a long context's split partials (AttnArgs::defer == 2), one wave per
+// query head: lane s holds split s's statistics (m_s, l_s), every lane DPL
+// output dims. out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with
+// w_s = 2^(m_s - max m) (0 for an empty split): the log-sum-exp merge of the
+// attention launch's own, with all of a head's partial loads in flight at once
+// and the query heads spread over many waves instead of one workgroup per KV head.
+template <int DPL, int MAXS>
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float* part, int ns, int G, int hkv, float* out) {
+    constexpr int HD = 64 * DPL;
+    const int wv = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wv >= hkv * G) return;   // wave-uniform
+    const int j = wv / G, gg = wv % G, rec = G * HD + 2 * G;
+    const float* kv = part + (size_t)j * ns * rec;
+    const int sl = min(lane, ns - 1);
+    const float m = lane < ns ? kv[(size_t)sl * rec + G * HD + gg] : -INFINITY;
+    const float l = lane < ns ? kv[(size_t)sl * rec + G * HD + G + gg] : 0.f;
+    float o[MAXS][DPL];
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) {
+        const float* src = kv + (size_t)min(s, ns - 1) * rec + gg * HD + lane * DPL;
+#pragma unroll
+        for (int i = 0; i < DPL; i++) o[s][i] = src[i];
+    }
+    const float mx = wave_max(m);
+    const float w = m == -INFINITY ? 0.f : exp2f(m - mx);
+    const float den = wave_sum(w * l);
+    float acc[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; i++) acc[i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < MAXS; s++) {
+        const float ws = __shfl(w, s);   // 0 for s >= ns
+#pragma unroll
+        for (int i = 0; i < DPL; i++) acc[i] = fmaf(ws, o[s][i], acc[i]);
+    }
+    const float inv = 1.0f / den;
+#pragma unroll
+    for (int i = 0; i < DPL; i++) out[(size_t)wv * HD + lane * DPL + i] = acc[i] * inv;
+}
+
+hipError_t launch_attention_merge(const AttnArgs& a, hipStream_t st) {
+    const int G = a.hq / a.hkv, ns = a.n_splits;
+    if (ns <= kDeferMaxSplits || ns > kMergeMaxSplits || a.hkv < 1 || a.hq % a.hkv) return hipErrorInvalidValue;
+    const dim3 grid((a.hq + 3) / 4);
+#define RIBN_MERGE(D)                                                                                             \
+    if (a.hd == 64 * D) {                                                                                         \
+        if (ns <= 16) attention_merge_kernel<D, 16><<<grid, 256, 0, st>>>(a.part, ns, G, a.hkv, a.out);          \
+        else if (ns <= 32) attention_merge_kernel<D, 32><<<grid, 256, 0, st>>>(a.part, ns, G, a.hkv, a.out);     \
+        else attention_merge_kernel<D, 64><<<grid, 256, 0, st>>>(a.part, ns, G, a.hkv, a.out);                   \
+        return hipGetLastError();                                                                                 \
+    }
+    RIBN_MERGE(1) RIBN_MERGE(2)
+#undef RIBN_MERGE
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
     if (a.n_splits < 1 || a.n_splits > kMaxSplits || a.hkv < 1 || a.hq % a.hkv || a.rot > a.hd || a.rot % 2)
         return hipErrorInvalidValue;
-    if (a.defer && a.n_splits > kDeferMaxSplits) return hipErrorInvalidValue;
+    if (a.defer == 1 && a.n_splits > kDeferMaxSplits) return hipErrorInvalidValue;
+    if (a.defer == 2 && (a.n_splits <= kDeferMaxSplits || a.n_splits > kMergeMaxSplits || (a.hd != 64 && a.hd != 128)))
+        return hipErrorInvalidValue;
     if (a.hd == 128) return a.kv_f16 ? attention_dispatch<128, true>(a, st) : attention_dispatch<128, false>(a, st);
     if (a.hd == 64) return a.kv_f16 ? attention_dispatch<64, true>(a, st) : attention_dispatch<64, false>(a, st);
     if (a.hd == 256) return a.kv_f16 ? attention_dispatch<256, true>(a, st) : attention_dispatch<256, false>(a, st);

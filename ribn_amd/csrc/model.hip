@@ -141,6 +141,7 @@ struct ribn_rocm_model {
     uint16_t *p_x16 = nullptr, *p_att16 = nullptr, *p_act16 = nullptr;
     // integer-dot decode (RIBN_LOAD_INT_DOT): Q8_1 words of the decode rows' inputs, SwiGLU rows
     bool int_dot = false;
+    bool merge_in_launch = false;   // RIBN_LOAD_ATTN_MERGE_IN_LAUNCH: long-context split partials merged in the attention launch
     uint32_t* b_xq = nullptr;
     float* b_act = nullptr;
     int cur_slot = 0;   // the slot select_slot last pointed the step at
@@ -568,6 +569,13 @@ void build_launches(ribn_rocm_model* M) {
     M->mv_head = hdv;
 }
 
+// The bs1 chain merges more than kDeferMaxSplits split partials in a separate
+// launch (attention_merge_kernel) when the geometry allows it.
+bool merge_apart_for(const ribn_rocm_model* M, int n_splits) {
+    return !M->hybrid && !M->merge_in_launch && n_splits > kDeferMaxSplits && n_splits <= kMergeMaxSplits &&
+           (M->hd == 64 || M->hd == 128);
+}
+
 AttnArgs attn_args(ribn_rocm_model* M, int l, int n_splits) {
     AttnArgs at{};
     const Layer& y = M->layers[l];
@@ -718,6 +726,10 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
     // trips. Gated attention multiplies the merged output first, so hybrids merge
     // in the attention launch.
     const bool defer = !M->hybrid && n_splits > 1 && n_splits <= kDeferMaxSplits;
+    // Long contexts (more splits than the projection merges) merge the partials
+    // in a launch of their own, one wave per query head: the attention launch's
+    // last workgroup per KV head took ~10 us for 32 splits at G = 8.
+    const bool merge_apart = merge_apart_for(M, n_splits);
     for (int l = 0; l < M->L; l++) {
         const Layer& y = M->layers[l];
         if ((e = launch_matvec(M->mv_qkv[l], M->wg_qkv[l], st)) != hipSuccess) return e;
@@ -726,8 +738,9 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
         } else {
             if (M->hybrid && (e = launch_matvec(M->mv_aux[l], M->wg_aux[l], st)) != hipSuccess) return e;
             at = attn_args(M, l, n_splits);
-            at.defer = defer ? 1 : 0;
+            at.defer = defer ? 1 : merge_apart ? 2 : 0;
             if ((e = launch_attention(at, st)) != hipSuccess) return e;
+            if (merge_apart && (e = launch_attention_merge(at, st)) != hipSuccess) return e;
             if (M->hybrid && (e = launch_gate_mul(M->attn, M->att_gate, M->hq * M->hd, st)) != hipSuccess) return e;
         }
         MvArgs o = M->mv_o[l];
@@ -1413,6 +1426,7 @@ extern "C" int ribn_rocm_load_gguf(const char* path, const ribn_rocm_load_option
     const int qd = M->hq * M->hd, kd = M->hkv * M->hd;
     // matrices the GEMMs read also get the GEMM-ordered copy (not the embedding table)
     const bool gemm_copy = !(o.flags & RIBN_LOAD_GEMM_FROM_PLANES);
+    M->merge_in_launch = (o.flags & RIBN_LOAD_ATTN_MERGE_IN_LAUNCH) != 0;
     auto upload_mat = [&](const GgufTensor* t, uint64_t rows, uint64_t k, QMat* q) -> int {
         if (t->dims.size() != 2 || t->dims[0] != k || t->dims[1] != rows) {
             return fail(nullptr, err, err_len,
@@ -2376,9 +2390,17 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
         hipEvent_t e0, e1;
         HIPCHK(hipEventCreate(&e0));
         HIPCHK(hipEventCreate(&e1));
-        for (int i = 0; i < 3; i++) HIPCHK(launch_attention(at, M->stream));
+        // as in the decode chain: long contexts merge in a launch of their own
+        const bool apart = merge_apart_for(M, at.n_splits);
+        at.defer = apart ? 2 : 0;
+        auto run = [&]() -> hipError_t {
+            hipError_t e2 = launch_attention(at, M->stream);
+            if (e2 == hipSuccess && apart) e2 = launch_attention_merge(at, M->stream);
+            return e2;
+        };
+        for (int i = 0; i < 3; i++) HIPCHK(run());
         HIPCHK(hipEventRecord(e0, M->stream));
-        for (uint32_t i = 0; i < iters; i++) HIPCHK(launch_attention(at, M->stream));
+        for (uint32_t i = 0; i < iters; i++) HIPCHK(run());
         HIPCHK(hipEventRecord(e1, M->stream));
         HIPCHK(hipEventSynchronize(e1));
         float ms = 0.f;

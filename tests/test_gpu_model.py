@@ -225,8 +225,9 @@ def test_long_prefill_wide_attention(tmp_path, g, kv):
 @pytest.mark.parametrize("kv", list(KV_MODES))
 def test_split_policy_regimes(tmp_path, kv):
     """8400 positions through every regime of the split policy: one workgroup up to 128 positions, then
-    splits of about 128 (up to 2048), 256 (up to 8192) and 1024 positions (flash-decoding blocks across a
-    whole 1024-position split); logits at each boundary and at the end against the FP32 oracle. One layer,
+    splits of about 128 (up to 2048), 256 (up to 8192), then 32 splits of up to 263 positions merged by the
+    separate merge launch (head_dim 64: one output dim per lane); logits at each boundary and at the end
+    against the FP32 oracle. One layer,
     one KV head, Q8_0, so the oracle's quadratic attention stays within seconds."""
     path = str(tmp_path / "long.gguf")
     ribn_amd.synth_qwen_gguf(path, qwen3=False, hidden=128, layers=1, q_heads=2, kv_heads=1, head_dim=64, ffn=256,
@@ -498,11 +499,13 @@ def test_executor_contract_errors(model_paths):
 
 
 # ---------------------------------------------------------------- configs[3] / configs[4] regimes
+@pytest.mark.parametrize("merge", ["apart", "in-launch"])
 @pytest.mark.parametrize("kv", list(KV_MODES))
-def test_configs4_attention_32_splits_g8_hd128(tmp_path, kv):
+def test_configs4_attention_32_splits_g8_hd128(tmp_path, kv, merge):
     """configs[4]'s attention geometry (8 query heads per KV head, head_dim 128) at 16,500 positions:
-    32 splits of up to 1024 positions, merged in batches of 8 splits (four merge batches); also 4096 and
-    8192 positions (32 splits of 128 / 256) and 8193+ (16 splits of 1024). One layer, so the oracle appends
+    32 splits of up to 1024 positions (also at 4096 and 8192 positions: 32 splits of 128 / 256), merged by
+    the separate merge launch (one wave per query head) or, in-launch, by the attention launch's last
+    workgroup per KV head in batches of 8 splits (four merge batches). One layer, so the oracle appends
     K/V only at unchecked positions (orc_qwen_append_kv) and runs the full forward at the checked ones."""
     path = str(tmp_path / "c4attn.gguf")
     ribn_amd.synth_qwen_gguf(path, qwen3=True, hidden=256, layers=1, q_heads=8, kv_heads=1, head_dim=128, ffn=256,
@@ -512,8 +515,8 @@ def test_configs4_attention_32_splits_g8_hd128(tmp_path, kv):
     tokens = np.random.default_rng(8).integers(0, 256, n).tolist()
     windows = [(4088, 4100), (8186, 8200), (16380, 16392), (n - 12, n)]
     check = set(p for lo, hi in windows for p in range(lo, hi))
-    say(f"configs[4] attention geometry: trace {n} tokens kv={kv}")
-    with ribn_amd.QwenRocm(path, context_tokens=n + 16, max_sequences=1, kv=kv) as m:
+    say(f"configs[4] attention geometry: trace {n} tokens kv={kv} merge={merge}")
+    with ribn_amd.QwenRocm(path, context_tokens=n + 16, max_sequences=1, kv=kv, attn_merge=merge) as m:
         _, lg, _ = m.trace(tokens, logits=True)
     o = orc.QwenOracle(path, max_ctx=n + 16, kv_round=kv_round)
     ref = {}
