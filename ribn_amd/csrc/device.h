@@ -782,7 +782,7 @@ __device__ __forceinline__ bool mv_run(const MvArgs& a, const MvSeg& sg, WaveWor
     // depth: one that divides the wave's group count (no refill past the end),
     // or the full depth when the count is large enough for a few reloads of the
     // last group not to matter
-    if constexpr (R == 1 && P >= 2 && std::remove_reference_t<Sync>::kEarlyX && T != 8) {
+    if constexpr (R == 1 && P >= 2 && std::remove_reference_t<Sync>::kEarlyX) {
         if (w.ngr == 2 && w.n_units - 128 <= 32)
             return mv_ring<T, MODE, 2, R, std::remove_reference_t<Sync>&, true>(a, sg, w, xs, gs, red, rb, best, sync);
     }

@@ -94,7 +94,8 @@ def _ref_rows(t, blocks, rows, k, x, idx=None):
     (12, 1001, 4096), (14, 999, 4096), (8, 1003, 896), (8, 257, 4864), (14, 300, 12288), (12, 64, 5120),
     (12, 3, 256), (8, 1, 32),
     # rows of 129-160 units: a full load group and a tail group of one unit per lane
-    (14, 71, 5120), (12, 41, 4352), (14, 33, 4608), (12, 1, 4864),
+    (14, 71, 5120), (12, 41, 4352), (14, 33, 4608), (12, 1, 4864), (8, 67, 2560),
+    (8, 45, 1024), (12, 37, 2048), (14, 5, 512),
 ])
 def test_matvec_vs_fp64(t, rows, k):
     say(f"matvec t={t} rows={rows} k={k}")
