@@ -273,8 +273,13 @@ int ribn_rocm_argmax_noalloc(const float *d_logits, uint64_t n, uint32_t *d_out,
  * times on the model's stream: which = 0 fused gate/up (SwiGLU) of layer 0,
  * 1 ffn_down, 2 output head, 3 and 4 fused QKV, 5 attn_output, 6 decode attention of layer 0 (pass the context
  * length in the low 32 bits of *bytes and, in the high 32 bits, a split count to use instead of the default, or 0; the scratch sequence must hold that many positions, e.g.
- * after ribn_rocm_generate). *avg_ms per launch; *bytes = encoded weight bytes
- * one launch streams (0 for attention). */
+ * after ribn_rocm_generate), 7 every layer's fused gate/up inside graph-replayed decode
+ * steps, from its first workgroup's start to its last workgroup's end on the device
+ * wall clock (the launch chain with the other launches in between; pass the
+ * starting context in the low 32 bits of *bytes; the steps run on a scratch
+ * sequence).
+ * *avg_ms per launch; *bytes = encoded weight bytes one launch streams (0 for
+ * attention). */
 int ribn_rocm_bench_model_kernel(ribn_rocm_model *model, uint32_t which, uint32_t iters, double *avg_ms,
                                  uint64_t *bytes, char *err, size_t err_len);
 

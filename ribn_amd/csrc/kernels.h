@@ -299,6 +299,10 @@ size_t matvec_lds_bytes(int k, int rows = 1);
 int matvec_max_rows(int k);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_attention_merge(const AttnArgs& a, hipStream_t stream);
+// Timing variant of a gate/up (MV_SILU) matvec launch: also folds the launch's
+// first workgroup start and last workgroup end (wall-clock ticks) into clk[0]
+// (atomic min; start it at UINT64_MAX) and clk[1] (atomic max; start it at 0).
+hipError_t launch_matvec_clocked(const MvArgs& a, int n_wg, unsigned long long* clk, hipStream_t stream);
 
 // Batched decode: one decode row per sequence, all in one step. Row r consumes
 // the token at position pos[r] of the sequence in slot slot[r]; its page table

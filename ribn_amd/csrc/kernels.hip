@@ -300,6 +300,24 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* part,
     for (int i = 0; i < DPL; i++) out[(size_t)wv * HD + lane * DPL + i] = acc[i] * inv;
 }
 
+hipError_t launch_matvec_clocked(const MvArgs& a, int n_wg, unsigned long long* clk, hipStream_t st) {
+    if (a.mode != MV_SILU || n_wg < 1 || !clk) return hipErrorInvalidValue;
+    const size_t lds = matvec_lds_bytes(a.k, 1);
+#define RIBN_MVC(A)                                                                                              \
+    if (a.type_a == A) {                                                                                         \
+        if (lds > 65536) {                                                                                       \
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&matvec_clocked_kernel<A, A, MV_SILU>), \
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);           \
+            if (e != hipSuccess) return e;                                                                       \
+        }                                                                                                        \
+        matvec_clocked_kernel<A, A, MV_SILU><<<n_wg, mv_waves(a) * 64, lds, st>>>(a, clk);                       \
+        return hipGetLastError();                                                                                \
+    }
+    RIBN_MVC(12) RIBN_MVC(14) RIBN_MVC(8)
+#undef RIBN_MVC
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_attention_merge(const AttnArgs& a, hipStream_t st) {
     const int G = a.hq / a.hkv, ns = a.n_splits;
     if (ns <= kDeferMaxSplits || ns > kMergeMaxSplits || a.hkv < 1 || a.hq % a.hkv) return hipErrorInvalidValue;

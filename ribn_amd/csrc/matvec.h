@@ -36,6 +36,18 @@ __global__ __launch_bounds__(kMaxMvThreads) void matvec_kernel(MvArgs a) {
     if constexpr (MODE == MV_HEAD) head_finish(a, best, blockIdx.x, gridDim.x);
 }
 
+// matvec_kernel with its first workgroup start and last workgroup end folded
+// into clk (timing only; kept apart so the product kernel carries no clock code).
+template <int TA, int TB, int MODE>
+__global__ __launch_bounds__(kMaxMvThreads) void matvec_clocked_kernel(MvArgs a, unsigned long long* clk) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint64_t best = 0ull;
+    if (threadIdx.x == 0) atomicMin(&clk[0], (unsigned long long)wall_clock64());
+    mv_wg<TA, TB, MODE, ring_standalone<TA>(), ring_standalone<TB>(), 1>(a, blockIdx.x, lds, best, NoSync{});
+    __syncthreads();
+    if (threadIdx.x == 0) atomicMax(&clk[1], (unsigned long long)wall_clock64());
+}
+
 inline int mv_waves(const MvArgs& a) { return a.waves ? a.waves : kWaves; }
 
 template <int MODE, int R = 1>

@@ -142,6 +142,7 @@ struct ribn_rocm_model {
     // integer-dot decode (RIBN_LOAD_INT_DOT): Q8_1 words of the decode rows' inputs, SwiGLU rows
     bool int_dot = false;
     bool merge_in_launch = false;   // RIBN_LOAD_ATTN_MERGE_IN_LAUNCH: long-context split partials merged in the attention launch
+    unsigned long long* gu_clk = nullptr;   // set only while ribn_rocm_bench_model_kernel 7 captures its step
     uint32_t* b_xq = nullptr;
     float* b_act = nullptr;
     int cur_slot = 0;   // the slot select_slot last pointed the step at
@@ -751,7 +752,9 @@ hipError_t enqueue_step(ribn_rocm_model* M, bool head, int n_splits, float* trac
             o.parts_hd = M->hd;
         }
         if ((e = launch_matvec(o, M->wg_o[l], st)) != hipSuccess) return e;
-        if ((e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st)) != hipSuccess) return e;
+        if (M->gu_clk) e = launch_matvec_clocked(M->mv_gu[l], M->wg_gu[l], M->gu_clk + 2 * l, st);
+        else e = launch_matvec(M->mv_gu[l], M->wg_gu[l], st);
+        if (e != hipSuccess) return e;
         if ((e = launch_matvec(M->mv_down[l], M->wg_down[l], st)) != hipSuccess) return e;
         if (trace &&
             (e = hipMemcpyAsync(trace + (size_t)(l + 1) * M->H, M->h, sizeof(float) * M->H, hipMemcpyDeviceToDevice, st)) !=
@@ -2383,6 +2386,75 @@ extern "C" int ribn_rocm_bench_model_kernel(ribn_rocm_model* M, uint32_t which, 
         at = attn_args(M, 0, force ? force : splits_for_ctx(ctx));
         *bytes = 0;
         break;
+    }
+    case 7: {
+        // every layer's gate/up launch inside graph-replayed decode steps of a
+        // scratch sequence holding `ctx` positions (weights streamed from HBM by
+        // the other launches in between, as in the decode loop)
+        const int ctx = (int)(*bytes & 0xffffffffu);
+        if (M->hybrid || M->step_wg) return fail(nullptr, err, err_len, "chain timing needs the dense launch chain", RIBN_ERR_INVALID);
+        if (ctx < 1 || (uint32_t)(ctx + iters + 1) > M->context)
+            return fail(nullptr, err, err_len, "chain timing context outside the prepared context", RIBN_ERR_INVALID);
+        if (!take_pages(M, (uint32_t)(ctx + iters + 1), &bench_pages))
+            return fail(nullptr, err, err_len, "not enough free KV pages", RIBN_ERR_CAPACITY);
+        const int slot = (int)M->max_seqs;
+        // token 0 at every position the steps embed (the embedding reads tokens[pos] unchecked)
+        const std::vector<uint32_t> toks((size_t)ctx + iters + 1, 0u);
+        HIPCHK(reset_slot(M, slot, bench_pages, toks.data(), (uint32_t)toks.size()));
+        M->h_state[slot].pos = ctx - 1;
+        HIPCHK(hipMemcpyAsync(&M->d_slots[slot], &M->h_state[slot], sizeof(SeqState), hipMemcpyHostToDevice, M->stream));
+        HIPCHK(select_slot(M, slot));
+        const int ns = splits_for_ctx(ctx + (int)iters);
+        if (splits_for_ctx(ctx) != ns) return fail(nullptr, err, err_len, "chain timing steps cross a split-count bucket", RIBN_ERR_INVALID);
+        // every gate/up launch (its timing variant) folds its first start and last
+        // end into its own pair of device words; captured into a graph of its
+        // own (the decode graphs run the plain kernel)
+        const int L = M->L;
+        unsigned long long* clk = nullptr;
+        HIPCHK(hipMalloc(&clk, sizeof(unsigned long long) * 2 * L));
+        struct ClkFree {
+            unsigned long long* p;
+            ~ClkFree() { hipFree(p); }
+        } clk_free{clk};
+        std::vector<unsigned long long> init(2 * L), got(2 * L);
+        for (int l = 0; l < L; l++) {
+            init[2 * l] = ~0ull;
+            init[2 * l + 1] = 0ull;
+        }
+        M->gu_clk = clk;
+        hipGraph_t g = nullptr;
+        hipError_t e1 = hipStreamBeginCapture(M->stream, hipStreamCaptureModeThreadLocal);
+        if (e1 == hipSuccess) {
+            e1 = enqueue_step(M, false, ns, nullptr);
+            const hipError_t e2 = hipStreamEndCapture(M->stream, &g);
+            if (e1 == hipSuccess) e1 = e2;
+        }
+        M->gu_clk = nullptr;
+        if (e1 != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            HIPCHK(e1);
+        }
+        hipGraphExec_t ex = nullptr;
+        const hipError_t e3 = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        HIPCHK(e3);
+        double ticks = 0.0;
+        hipError_t e4 = hipSuccess;
+        for (uint32_t i = 0; i < iters && e4 == hipSuccess; i++) {
+            e4 = hipMemcpy(clk, init.data(), sizeof(unsigned long long) * 2 * L, hipMemcpyHostToDevice);
+            if (e4 == hipSuccess) e4 = hipGraphLaunch(ex, M->stream);
+            if (e4 == hipSuccess) e4 = hipStreamSynchronize(M->stream);
+            if (e4 == hipSuccess) e4 = hipMemcpy(got.data(), clk, sizeof(unsigned long long) * 2 * L, hipMemcpyDeviceToHost);
+            for (int l = 0; l < L && e4 == hipSuccess; l++) ticks += (double)(got[2 * l + 1] - got[2 * l]);
+        }
+        hipGraphExecDestroy(ex);
+        HIPCHK(e4);
+        int khz = 0;
+        HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, M->device));
+        *avg_ms = ticks / ((double)iters * L) / (double)khz;
+        a = M->mv_gu[0];
+        *bytes = qbytes(a.seg[0].w) + qbytes(a.seg[0].w2);
+        return RIBN_OK;
     }
     default: return fail(nullptr, err, err_len, "unknown kernel selector", RIBN_ERR_INVALID);
     }

@@ -590,3 +590,17 @@ def test_8b_shape_layer_trace(tmp_path):
     say(f"  logits rel-L2 {r:.2e}")
     assert r <= REL_TOL
     _forced_argmax_check("8B layer", am, ref_l, 2 * float(np.abs(lg - ref_l).max()))
+
+
+def test_bench_gate_up_in_chain(model_paths):
+    """The in-chain timing of the gate/up launches (clocked launches in a captured step on a scratch sequence)
+    returns a positive time and the launch's weight bytes, and leaves the model usable."""
+    path = model_paths["qwen3_q4km_hd64"]
+    tokens = [3, 1, 4, 1, 5, 9, 2, 6]
+    with ribn_amd.QwenRocm(path, context_tokens=128, max_sequences=1) as m:
+        am0, lg0, _ = m.trace(tokens, logits=True)
+        ms, nbytes = m.bench_kernel(7, 3, 40)
+        assert ms > 0 and nbytes > 0
+        am1, lg1, _ = m.trace(tokens, logits=True)
+    assert np.array_equal(am0, am1)
+    np.testing.assert_array_equal(lg0, lg1)
