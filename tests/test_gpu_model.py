@@ -604,3 +604,28 @@ def test_bench_gate_up_in_chain(model_paths):
         am1, lg1, _ = m.trace(tokens, logits=True)
     assert np.array_equal(am0, am1)
     np.testing.assert_array_equal(lg0, lg1)
+
+
+def test_greedy_long_context_graph_merge(tmp_path):
+    """Greedy tokens of graph-replayed decode steps at 1100-1131 positions (16 attention splits: the split
+    partials merged by the separate merge launch inside the captured step) against the oracle
+    teacher-forced on the device's own stream, under the near-tie rule with the tolerance measured on
+    identical contexts (the device's teacher-forced trace)."""
+    path = str(tmp_path / "long_greedy.gguf")
+    ribn_amd.synth_qwen_gguf(path, qwen3=True, hidden=256, layers=1, q_heads=8, kv_heads=2, head_dim=64, ffn=256,
+                             vocab=256, seed=23, norm_jitter=0.15, weight_std=0.05, **Q4KM)
+    prompt = np.random.default_rng(9).integers(0, 256, 1100).tolist()
+    n_new = 32
+    ctx = len(prompt) + n_new + 8
+    with ribn_amd.QwenRocm(path, context_tokens=ctx, max_sequences=1) as m:
+        toks, timing = m.generate(prompt, n_new)
+        am, lg, _ = m.trace(prompt + toks.tolist()[:-1], logits=True)
+    assert timing.decode_tokens == n_new - 1
+    ref = _oracle_forced(path, prompt, toks.tolist(), ctx, kv_only_prompt=True)
+    dev = lg[len(prompt) - 1:]
+    r = _rel(dev, ref)
+    err = float(np.abs(dev - ref).max())
+    say(f"  same-context logits rel-L2 {r:.2e}, max abs err {err:.2e}")
+    assert r <= REL_TOL
+    _forced_argmax_check("trace", am[len(prompt) - 1:], ref, 2 * err)
+    _forced_argmax_check("generate", toks, ref, 4 * err)
